@@ -1,0 +1,47 @@
+/*
+ * MI355X extensions of the strix_trellis C ABI: stage checkpoints used by the
+ * parity tests.  None of these has a counterpart symbol in the reference
+ * header; they expose, through the same validation as the ABI calls, the
+ * intermediate results the reference's GPU tests compare byte for byte
+ * (decoded Q, core input, output stage from a known core:
+ * reference tests/gpu_runtime.hip:252-339, docs/GPU_TESTS.md:44-143).
+ * All buffers are device memory on the context device; every call enqueues on
+ * the given stream and returns without synchronising.
+ */
+#ifndef STRIX_TRELLIS_AMD_H
+#define STRIX_TRELLIS_AMD_H
+
+#include "strix_trellis.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Decoded FP16 Q[I][N] (row-major, input-major) of prepared weights.
+ * q_bytes >= 2*I*N.  Bit-exact with the transport's EXL3 decode. */
+strix_status strix_amd_decode(strix_weights weights, void *q_fp16, uint64_t q_bytes,
+    const strix_stream *stream);
+
+/* FP16 core input A[rows][I] = RN16(H32(RN16(RN32(x * suh)))) of F32 x[rows][I]. */
+strix_status strix_amd_input_stage(strix_weights weights, const float *x, uint64_t rows,
+    void *a_fp16, uint64_t a_bytes, const strix_stream *stream);
+
+/* Output stage from a known F32 core[rows][N]:
+ * y = alpha * (RN32(H32(core) * svh) [+ bias]) (+ beta * y_old iff beta != 0). */
+strix_status strix_amd_output_stage(strix_weights weights, const float *core, uint64_t rows,
+    float *y, uint64_t y_bytes, float alpha, float beta, const strix_stream *stream);
+
+/* Split decomposition of the GEMV core for these weights: input blocks of 16
+ * channels per split and the split count.  It fixes the core's accumulation
+ * order and depends only on the weight geometry. */
+strix_status strix_amd_gemv_shape(strix_weights weights, uint32_t *blocks_per_split,
+    uint32_t *splits);
+
+/* Kernel launches one submission of a prepared plan enqueues (1 for a
+ * single-launch GEMV plan). */
+strix_status strix_amd_plan_launches(strix_linear_plan plan, uint32_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* STRIX_TRELLIS_AMD_H */

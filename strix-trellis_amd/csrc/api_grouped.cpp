@@ -1,0 +1,196 @@
+// Grouped strided GEMV plans (reference include/strix_trellis.h:415-457,
+// src/dense_r1_group_api.inc:27-137).
+//
+//   output[r][g*ogs + n] = Linear_g(input[r][g*igs + i]),  alpha 1, beta 0, rows 1..8
+//
+// Every group runs the generic GEMV core of its geometry in one launch (grid z =
+// group), so each row has exactly the bits of that row submitted alone through
+// strix_gemv (STRIX_GEMV_ROW_INVARIANT_R1).  Workspace layout, all offsets a
+// function of the geometry only:
+//   [counters: kMaxGroups * N/128 u32][group table: kMaxGroups entries][partials: G * S * rows * N f32]
+// Creation uploads the table, zeroes the counters and synchronises the stream;
+// each completed submission leaves the counters zero again.
+#include "api_internal.hpp"
+
+#include <new>
+
+using namespace stx_api;
+
+namespace {
+constexpr uint64_t kMaxGroups = STRIX_TP_MAX_BANK_EXPERTS;
+constexpr uint64_t kAlign = STRIX_TRELLIS_WORKSPACE_ALIGNMENT;
+uint64_t align_up(uint64_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+struct GroupLayout {
+    uint64_t counter_bytes = 0, table_offset = 0, partial_offset = 0, bytes = 0;
+};
+
+struct Validated {
+    std::vector<strix_weights> weights;
+    stx::DeviceWeights geometry{};
+    uint64_t rows = 0, xrs = 0, xgs = 0, yrs = 0, ygs = 0;
+    uint64_t input_bytes = 0, output_bytes = 0;
+    GroupLayout layout{};
+};
+
+// Bytes up to the last F32 element touched by `count` views of `rows` rows of `width`.
+bool view_bytes(uint64_t rows, uint64_t row_stride, uint64_t count, uint64_t group_stride, uint64_t width,
+                uint64_t& out) {
+    uint64_t a = 0, b = 0;
+    if (!mul_ok(rows - 1, row_stride, a) || !mul_ok(count - 1, group_stride, b)) return false;
+    if (a > UINT64_MAX - b || a + b > UINT64_MAX - width) return false;
+    return mul_ok(a + b + width, 4, out);
+}
+
+strix_status validate(strix_context c, const strix_grouped_gemv_desc* d, Validated& v) {
+    strix_status s = check_header(d);
+    if (s != STRIX_SUCCESS) return s;
+    if (!d->weights || d->group_count < 1 || d->group_count > kMaxGroups || d->rows < 1 || d->rows > 8 ||
+        d->flags != STRIX_GEMV_ROW_INVARIANT_R1 || !d->input || !d->output)
+        return STRIX_ERROR_INVALID_ARGUMENT;
+    const uint64_t G = d->group_count;
+    v.weights.assign(d->weights, d->weights + G);
+    for (uint64_t g = 0; g < G; ++g) {
+        const strix_weights w = v.weights[g];
+        if (!w || w->owner != c) return STRIX_ERROR_INVALID_ARGUMENT;
+        const stx::DeviceWeights& dw = w->dev;
+        if (g == 0) {
+            v.geometry = dw;
+        } else if (dw.bits != v.geometry.bits || dw.input != v.geometry.input || dw.output != v.geometry.output ||
+                   dw.codebook != v.geometry.codebook) {
+            return STRIX_ERROR_UNSUPPORTED_FORMAT;
+        }
+        if (w->plans == UINT64_MAX) return STRIX_ERROR_OUT_OF_MEMORY;
+    }
+    const uint64_t rows = d->rows, I = v.geometry.input, N = v.geometry.output;
+    v.rows = rows;
+    v.xrs = rows > 1 ? d->input_row_stride : 0;
+    v.xgs = G > 1 ? d->input_group_stride : 0;
+    v.yrs = rows > 1 ? d->output_row_stride : 0;
+    v.ygs = G > 1 ? d->output_group_stride : 0;
+    if ((rows > 1 && v.xrs < I) || (G > 1 && v.ygs < N) || (rows > 1 && v.yrs < (G - 1) * v.ygs + N))
+        return STRIX_ERROR_INVALID_ARGUMENT;
+    if (!view_bytes(rows, v.xrs, G, v.xgs, I, v.input_bytes) || !view_bytes(rows, v.yrs, G, v.ygs, N, v.output_bytes) ||
+        v.input_bytes > d->input_buffer_bytes || v.output_bytes > d->output_buffer_bytes ||
+        reinterpret_cast<uintptr_t>(d->input) % 4 || reinterpret_cast<uintptr_t>(d->output) % 4 ||
+        !span_ok(d->input, v.input_bytes) || !span_ok(d->output, v.output_bytes) ||
+        overlaps(d->input, v.input_bytes, d->output, v.output_bytes))
+        return STRIX_ERROR_INVALID_ARGUMENT;
+    for (strix_weights w : v.weights)
+        if (overlaps(d->input, v.input_bytes, w->base, w->bytes) || overlaps(d->output, v.output_bytes, w->base, w->bytes))
+            return STRIX_ERROR_INVALID_ARGUMENT;
+    const stx::GemvShape sh = stx::gemv_shape(uint32_t(I), uint32_t(N), v.geometry.bits);
+    GroupLayout& L = v.layout;
+    L.counter_bytes = (N / 128) * 4;
+    L.table_offset = align_up(kMaxGroups * L.counter_bytes);
+    L.partial_offset = L.table_offset + align_up(kMaxGroups * sizeof(stx::GroupWeights));
+    const uint64_t planes = sh.splits > 1 ? uint64_t(sh.splits) * rows * N * 4 : 0;
+    L.bytes = L.partial_offset + align_up(planes * G);
+    return STRIX_SUCCESS;
+}
+}  // namespace
+
+struct strix_grouped_gemv_plan_impl {
+    strix_context owner = nullptr;
+    std::vector<strix_weights> retained;
+    stx::DeviceWeights geometry{};
+    stx::LinearCall call{};
+    const stx::GroupWeights* table = nullptr;
+    uint32_t* counters = nullptr;
+    uint64_t xgs = 0, ygs = 0;
+    hipStream_t stream{};
+};
+
+extern "C" {
+
+strix_status strix_grouped_gemv_workspace_bytes(strix_context c, const strix_grouped_gemv_desc* d, uint64_t* out) {
+    if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
+    *out = 0;
+    strix_status s = context_ok(c);
+    if (s != STRIX_SUCCESS) return s;
+    Validated v;
+    s = validate(c, d, v);
+    if (s == STRIX_SUCCESS) *out = v.layout.bytes;
+    return s;
+}
+
+strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped_gemv_desc* d,
+                                            const strix_stream* stream, strix_grouped_gemv_plan* out) {
+    if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
+    *out = nullptr;
+    strix_status s = context_ok(c);
+    if (s != STRIX_SUCCESS) return s;
+    hipStream_t hs{};
+    s = stream_ok(c, stream, hs);
+    if (s != STRIX_SUCCESS) return s;
+    Validated v;
+    s = validate(c, d, v);
+    if (s != STRIX_SUCCESS) return s;
+    if (d->workspace_bytes < v.layout.bytes) return STRIX_ERROR_INSUFFICIENT_BUFFER;
+    if (!d->workspace || !span_ok(d->workspace, d->workspace_bytes) ||
+        reinterpret_cast<uintptr_t>(d->workspace) % kAlign ||
+        overlaps(d->workspace, d->workspace_bytes, d->input, v.input_bytes) ||
+        overlaps(d->workspace, d->workspace_bytes, d->output, v.output_bytes))
+        return STRIX_ERROR_INVALID_ARGUMENT;
+    for (strix_weights w : v.weights)
+        if (overlaps(d->workspace, d->workspace_bytes, w->base, w->bytes)) return STRIX_ERROR_INVALID_ARGUMENT;
+    if ((s = device_range_ok(c, d->input, v.input_bytes, 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_range_ok(c, d->output, v.output_bytes, 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_range_ok(c, d->workspace, d->workspace_bytes, kAlign)) != STRIX_SUCCESS) return s;
+
+    auto* p = new (std::nothrow) strix_grouped_gemv_plan_impl;
+    if (!p) return STRIX_ERROR_OUT_OF_MEMORY;
+    std::vector<stx::GroupWeights> table;
+    try {
+        p->retained = v.weights;
+        for (strix_weights w : v.weights) table.push_back({w->dev.trellis, w->dev.suh, w->dev.svh, w->dev.bias});
+    } catch (...) {
+        delete p;
+        return STRIX_ERROR_OUT_OF_MEMORY;
+    }
+    char* base = static_cast<char*>(d->workspace);
+    p->counters = reinterpret_cast<uint32_t*>(base);
+    p->table = reinterpret_cast<const stx::GroupWeights*>(base + v.layout.table_offset);
+    hipError_t e = hipMemcpyAsync(base + v.layout.table_offset, table.data(), table.size() * sizeof(table[0]),
+                                  hipMemcpyHostToDevice, hs);
+    if (e == hipSuccess)
+        e = stx::launch_fill_u32(p->counters, 0, v.layout.counter_bytes / 4 * v.weights.size(), hs);
+    const hipError_t done = hipStreamSynchronize(hs);
+    if (e != hipSuccess || done != hipSuccess) {
+        delete p;
+        return from_hip(e != hipSuccess ? e : done);
+    }
+    p->owner = c;
+    p->geometry = v.geometry;
+    p->stream = hs;
+    p->xgs = v.xgs;
+    p->ygs = v.ygs;
+    p->call.x = d->input;
+    p->call.y = d->output;
+    p->call.rows = v.rows;
+    p->call.x_row_stride = v.xrs;
+    p->call.y_row_stride = v.yrs;
+    p->call.alpha = 1.0f;
+    p->call.beta = 0.0f;
+    p->call.workspace = base + v.layout.partial_offset;
+    for (strix_weights w : v.weights) ++w->plans;
+    *out = p;
+    return STRIX_SUCCESS;
+}
+
+strix_status strix_grouped_gemv_plan_submit(strix_grouped_gemv_plan p) {
+    if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
+    const strix_status s = context_ok(p->owner);
+    if (s != STRIX_SUCCESS) return s;
+    return from_hip(stx::launch_gemv_grouped(p->geometry, p->table, uint32_t(p->retained.size()), p->call, p->xgs,
+                                             p->ygs, p->counters, p->stream));
+}
+
+strix_status strix_grouped_gemv_plan_destroy(strix_grouped_gemv_plan p) {
+    if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
+    for (strix_weights w : p->retained) --w->plans;
+    delete p;
+    return STRIX_SUCCESS;
+}
+
+}  // extern "C"

@@ -1,0 +1,84 @@
+// Internal interface between the C ABI layer (api.cpp) and the HIP kernels.
+// Plain structs and host launch functions; nothing here is part of the ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace stx {
+
+// Prepared weights as the kernels see them (one private device allocation).
+struct DeviceWeights {
+    const uint32_t* trellis = nullptr;   // [I/16][N/16][8K] u32, transport order
+    const uint16_t* suh = nullptr;       // FP16 [I]
+    const uint16_t* svh = nullptr;       // FP16 [N]
+    const float* bias = nullptr;         // F32 [N] or null
+    uint32_t input = 0;                  // I
+    uint32_t output = 0;                 // N
+    uint32_t bits = 0;                   // K, 1..8
+    uint32_t codebook = 0;               // 0 3inst, 1 mcg, 2 mul1
+    uint64_t trellis_bytes = 0;
+};
+
+// Per-group weight pointers of a grouped launch (device-resident table).
+struct GroupWeights {
+    const uint32_t* trellis;
+    const uint16_t* suh;
+    const uint16_t* svh;
+    const float* bias;
+};
+
+// GEMV decomposition (a function of I, N and K only, never of the row count,
+// so every row has the same bits whatever rows are submitted with it).
+struct GemvShape {
+    uint32_t bps = 0;      // 16-row input blocks per split, multiple of 8
+    uint32_t splits = 0;   // S = (I/16) / bps
+};
+GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t bits);
+
+// Bytes of the caller workspace one call needs (GEMV partial planes and the
+// FP16 core-input matrix of the GEMM path); 256-byte aligned pieces.
+uint64_t gemv_workspace_bytes(const DeviceWeights& w, uint32_t rows);
+uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows);
+uint64_t linear_workspace_bytes(const DeviceWeights& w, uint64_t rows);
+// Completion counters (u32) a single-launch GEMV needs: one per 128 outputs.
+uint32_t gemv_counter_count(const DeviceWeights& w);
+
+struct LinearCall {
+    const float* x = nullptr;
+    float* y = nullptr;
+    uint64_t rows = 0;
+    uint64_t x_row_stride = 0;   // elements
+    uint64_t y_row_stride = 0;
+    float alpha = 1.0f;
+    float beta = 0.0f;
+    void* workspace = nullptr;
+};
+
+// Generic GEMV (rows 1..8): core kernel + finishing kernel, no counters.
+hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
+// Single-launch GEMV: the last workgroup of each 128-output group finishes.
+// `counters` must be zero on entry; they are zero again when the launch ends.
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, uint32_t* counters,
+                             hipStream_t stream);
+// Grouped GEMV over `groups` weights of one geometry (table in device memory).
+hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
+                               const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
+                               uint32_t* counters, hipStream_t stream);
+// Prefill path (any row count): input stage to FP16 in the workspace, then the
+// MFMA core with the fused output stage.
+hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
+uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows);
+uint32_t linear_launch_count(const DeviceWeights& w, uint64_t rows, bool gemm, bool counters);
+// Dispatch used by strix_gemv / strix_gemm / grouped MoE.
+hipError_t launch_linear(const DeviceWeights& w, const LinearCall& call, bool prefer_gemm, hipStream_t stream);
+
+// Diagnostics for parity tests (exported through strix_trellis_amd.h).
+hipError_t launch_decode(const DeviceWeights& w, _Float16* q, hipStream_t stream);
+hipError_t launch_input_stage(const DeviceWeights& w, const float* x, uint64_t rows, _Float16* a,
+                              hipStream_t stream);
+hipError_t launch_output_stage(const DeviceWeights& w, const float* core, uint64_t rows, float* y,
+                               float alpha, float beta, hipStream_t stream);
+hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStream_t stream);
+
+}  // namespace stx

@@ -1,0 +1,173 @@
+// Host side of the decode GEMV: decomposition, workspace, launches; plus the
+// finishing kernel and the diagnostic stage kernels.
+#include "gemv_kernel.hpp"
+
+namespace stx {
+
+// Split decomposition.  The whole matrix must be in flight at once for the
+// small decode shapes (8 MiB at K4 4096^2 is about one HBM latency-bandwidth
+// product), so aim for >= 1024 workgroups of 4 waves; among candidate splits
+// (bps = 8m with m dividing (I/16)/8, m <= 16) take the largest bps that keeps
+// the grid at or above that target, else the smallest bps.
+GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t /*bits*/) {
+    const uint32_t nb = input / 16, nc = output / 128, units = nb / 8;
+    constexpr uint32_t target = 1024;
+    GemvShape best{8, nb / 8};
+    for (uint32_t m = 1; m <= 16; ++m) {
+        if (units % m) continue;
+        const uint32_t bps = 8 * m, splits = nb / bps;
+        if (uint64_t(nc) * splits >= target) best = {bps, splits};
+    }
+    return best;
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+
+uint64_t gemv_workspace_bytes(const DeviceWeights& w, uint32_t rows) {
+    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
+    if (sh.splits <= 1) return 0;
+    return align256(uint64_t(sh.splits) * rows * w.output * sizeof(float));
+}
+
+uint32_t gemv_counter_count(const DeviceWeights& w) {
+    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
+    return sh.splits > 1 ? w.output / 128 : 0;
+}
+
+static uint32_t rows_template(uint64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
+
+using GemvDispatch = hipError_t (*)(const GemvLaunch&);
+static const GemvDispatch gemv_table[8] = {gemv_dispatch<1>, gemv_dispatch<2>, gemv_dispatch<3>,
+                                           gemv_dispatch<4>, gemv_dispatch<5>, gemv_dispatch<6>,
+                                           gemv_dispatch<7>, gemv_dispatch<8>};
+
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
+    const int c = blockIdx.x, z = blockIdx.z;
+    const GroupWeights gw = group_weights(a, z);
+    float* y = a.y + z * a.y_group_stride;
+    const float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
+    finish_columns(a, gw, y, c, a.splits, [&](int s, int r) -> const float* {
+        return plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c;
+    });
+}
+
+static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table, uint32_t groups,
+                              const LinearCall& call, uint64_t xg, uint64_t yg, uint32_t* counters,
+                              uint32_t mode, hipStream_t stream) {
+    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
+    GemvLaunch l{};
+    GemvArgs& a = l.args;
+    a.w = {w.trellis, w.suh, w.svh, w.bias};
+    a.table = table;
+    a.x = call.x;
+    a.y = call.y;
+    a.partials = static_cast<float*>(call.workspace);
+    a.counters = counters;
+    a.x_row_stride = call.x_row_stride;
+    a.y_row_stride = call.y_row_stride;
+    a.x_group_stride = xg;
+    a.y_group_stride = yg;
+    a.I = w.input;
+    a.N = w.output;
+    a.rows = uint32_t(call.rows);
+    a.splits = sh.splits;
+    a.bps = sh.bps;
+    a.alpha = call.alpha;
+    a.beta = call.beta;
+    a.mode = mode;
+    l.rows_template = rows_template(call.rows);
+    l.grid = dim3(w.output / 128, sh.splits, groups);
+    l.codebook = w.codebook;
+    l.lds = size_t(l.rows_template) * (32u * sh.bps + 2048u);
+    l.stream = stream;
+    return l;
+}
+
+hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream) {
+    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, nullptr, 0, stream);
+    hipError_t e = gemv_table[w.bits - 1](l);
+    if (e != hipSuccess || l.args.splits == 1) return e;
+    hipLaunchKernelGGL(gemv_finish_kernel, dim3(w.output / 128, 1, 1), dim3(GEMV_THREADS), 0, stream, l.args);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, uint32_t* counters,
+                             hipStream_t stream) {
+    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, counters, 1, stream);
+    return gemv_table[w.bits - 1](l);
+}
+
+hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
+                               const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
+                               uint32_t* counters, hipStream_t stream) {
+    GemvLaunch l = make_launch(geometry, table, groups, call, x_group_stride, y_group_stride, counters,
+                               counters ? 1 : 0, stream);
+    hipError_t e = gemv_table[geometry.bits - 1](l);
+    if (e != hipSuccess || counters || l.args.splits == 1) return e;
+    hipLaunchKernelGGL(gemv_finish_kernel, dim3(geometry.output / 128, 1, groups), dim3(GEMV_THREADS), 0,
+                       stream, l.args);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Diagnostics and utilities.
+// ---------------------------------------------------------------------------
+using DecodeDispatch = hipError_t (*)(uint32_t, const uint32_t*, uint32_t, uint32_t, uint64_t, _Float16*,
+                                      hipStream_t);
+static const DecodeDispatch decode_table[8] = {decode_dispatch<1>, decode_dispatch<2>, decode_dispatch<3>,
+                                               decode_dispatch<4>, decode_dispatch<5>, decode_dispatch<6>,
+                                               decode_dispatch<7>, decode_dispatch<8>};
+
+hipError_t launch_decode(const DeviceWeights& w, _Float16* q, hipStream_t stream) {
+    return decode_table[w.bits - 1](w.codebook, w.trellis, w.input, w.output, w.trellis_bytes, q, stream);
+}
+
+__global__ __launch_bounds__(64) void input_stage_kernel(const float* x, const uint16_t* suh, uint32_t I,
+                                                         _Float16* out) {
+    const uint64_t r = blockIdx.y;
+    const uint32_t ch = blockIdx.x * 128;
+    input_block(x + r * I + ch, suh + ch, out + r * I + ch, true);
+}
+
+hipError_t launch_input_stage(const DeviceWeights& w, const float* x, uint64_t rows, _Float16* a,
+                              hipStream_t stream) {
+    if (!rows) return hipSuccess;
+    hipLaunchKernelGGL(input_stage_kernel, dim3(w.input / 128, rows), dim3(64), 0, stream, x, w.suh, w.input, a);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(64) void output_stage_kernel(const float* core, const uint16_t* svh,
+                                                          const float* bias, uint32_t N, float alpha,
+                                                          float beta, float* y) {
+    const uint64_t r = blockIdx.y;
+    const int lane = threadIdx.x;
+    const uint32_t n0 = blockIdx.x * 128 + lane, n1 = n0 + 64;
+    float z0 = core[r * N + n0], z1 = core[r * N + n1];
+    h32_wave(z0, z1);
+    float* yr = y + r * N;
+    const float o0 = output_element(z0, svh[n0], bias, n0, alpha, beta, yr + n0);
+    const float o1 = output_element(z1, svh[n1], bias, n1, alpha, beta, yr + n1);
+    yr[n0] = o0;
+    yr[n1] = o1;
+}
+
+hipError_t launch_output_stage(const DeviceWeights& w, const float* core, uint64_t rows, float* y, float alpha,
+                               float beta, hipStream_t stream) {
+    if (!rows) return hipSuccess;
+    hipLaunchKernelGGL(output_stage_kernel, dim3(w.output / 128, rows), dim3(64), 0, stream, core, w.svh, w.bias,
+                       w.output, alpha, beta, y);
+    return hipGetLastError();
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t count) {
+    const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = value;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStream_t stream) {
+    if (!count) return hipSuccess;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(uint32_t((count + 255) / 256)), dim3(256), 0, stream, p, value, count);
+    return hipGetLastError();
+}
+
+}  // namespace stx

@@ -1,0 +1,6 @@
+// Decode GEMV and decode kernels for K = 1 bits per weight (all codebooks, 1/2/4/8-row templates).
+#include "gemv_kernel.hpp"
+
+namespace stx {
+STX_INSTANTIATE_GEMV(1)
+}  // namespace stx

@@ -1,0 +1,267 @@
+// Decode GEMV (rows 1..8) for gfx950: input stage, trellis decode + FP16 dot
+// with FP32 accumulation, split-K fold and output stage.
+//
+// Replaces the reference's generic GEMV family (src/gemv_lds.hip:14-168,
+// src/gemv_fused.hip:17-128, src/transforms.hpp:8-52) with one wave64 design:
+//
+//   grid (N/128, S, groups), block 256 = 4 waves.  Workgroup (c, s) owns
+//   output columns [128c, 128c+128) and input blocks [s*bps, (s+1)*bps)
+//   (16 channels each, bps a multiple of 8 so the split holds whole H128
+//   input blocks).
+//   * prologue: the workgroup computes the FP16 core input of its channels
+//     into LDS (one wave per 128-block); the first weight loads are issued
+//     before it so their latency overlaps it;
+//   * main loop: wave w takes input blocks w, w+4, ...; per block every lane
+//     loads its K-word chunk (K*256 contiguous bytes per wave), decodes 32
+//     weights in VGPRs and runs, per row, two v_dot2 chains (columns g, g+8)
+//     against activation pairs read from LDS by broadcast;
+//   * the four waves' partial sums meet in LDS and are added in wave order;
+//   * S == 1: the workgroup applies the output stage itself.  Otherwise it
+//     writes its [rows][128] partial plane; the finishing step (a second
+//     kernel, or with completion counters the last-arriving workgroup of the
+//     column group) folds the S planes in ascending split order from +0 and
+//     applies the output stage.
+//
+// Per-output accumulation order (defines the core's bits; depends on I, N,
+// K only, never on the row count):
+//   lane chain  : +0, then blocks in ascending order; within a block the dot2
+//                 pairs (rows 2V,2V+1) then (2V+8,2V+9) for V = 0..3;
+//   wave fold   : chain(w0) + chain(w1) + chain(w2) + chain(w3);
+//   split fold  : ((+0 + P0) + P1) + ... + P(S-1).
+#pragma once
+#include "backend.hpp"
+#include "stages.hpp"
+
+namespace stx {
+
+constexpr int GEMV_WAVES = 4;
+constexpr int GEMV_THREADS = 64 * GEMV_WAVES;
+
+struct GemvArgs {
+    GroupWeights w;               // weights of a single-group launch
+    const GroupWeights* table;    // per-group weights (grouped launch) or null
+    const float* x;
+    float* y;
+    float* partials;              // [groups][S][rows][N]
+    uint32_t* counters;           // [groups][N/128]
+    uint64_t x_row_stride, y_row_stride;
+    uint64_t x_group_stride, y_group_stride;
+    uint32_t I, N, rows, splits, bps;
+    float alpha, beta;
+    uint32_t mode;                // 0: partial planes only, 1: last workgroup finishes
+};
+
+__device__ __forceinline__ GroupWeights group_weights(const GemvArgs& a, int z) {
+    return a.table ? a.table[z] : a.w;
+}
+
+// Output stage of column group c for every row: fold, H32, epilogue.
+// `plane(s, r)` returns the pointer to the 128 values of split s, row r.
+template <typename Plane>
+__device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWeights& gw, float* y, int c,
+                                               int splits, Plane plane) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (uint32_t r = w; r < a.rows; r += GEMV_WAVES) {
+        float z0 = 0.0f, z1 = 0.0f;
+        for (int s = 0; s < splits; ++s) {
+            const float* p = plane(s, r);
+            z0 = z0 + p[lane];
+            z1 = z1 + p[lane + 64];
+        }
+        h32_wave(z0, z1);
+        const int n0 = 128 * c + lane, n1 = n0 + 64;
+        float* yr = y + r * a.y_row_stride;
+        const float o0 = output_element(z0, gw.svh[n0], gw.bias, n0, a.alpha, a.beta, yr + n0);
+        const float o1 = output_element(z1, gw.svh[n1], gw.bias, n1, a.alpha, a.beta, yr + n1);
+        yr[n0] = o0;
+        yr[n1] = o1;
+    }
+}
+
+template <int K, int CB, int RT>
+__device__ __forceinline__ void gemv_block(const Chunk<K>& chunk, const _Float16* act, uint32_t act_row,
+                                           float (&acc)[RT][2]) {
+    half2_t wq[4][4];
+    decode_chunk<K, CB>(chunk, wq);
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(act + r * act_row);
+        const u32x4 lo = p[0], hi = p[1];
+        const half2_t xp[8] = {as_h2(lo.x), as_h2(lo.y), as_h2(lo.z), as_h2(lo.w),
+                               as_h2(hi.x), as_h2(hi.y), as_h2(hi.z), as_h2(hi.w)};
+        float a0 = acc[r][0], a1 = acc[r][1];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            a0 = __builtin_amdgcn_fdot2(wq[v][0], xp[v], a0, false);
+            a0 = __builtin_amdgcn_fdot2(wq[v][1], xp[v + 4], a0, false);
+            a1 = __builtin_amdgcn_fdot2(wq[v][2], xp[v], a1, false);
+            a1 = __builtin_amdgcn_fdot2(wq[v][3], xp[v + 4], a1, false);
+        }
+        acc[r][0] = a0;
+        acc[r][1] = a1;
+    }
+}
+
+template <int K, int CB, int RT>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int last_flag;
+    const int c = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int jt = lane >> 3, g = lane & 7;
+    const GroupWeights gw = group_weights(a, z);
+    const float* x = a.x + z * a.x_group_stride;
+    float* y = a.y + z * a.y_group_stride;
+
+    constexpr uint32_t tile_bytes = 32u * K;
+    const uint32_t row_bytes = (a.N >> 4) * tile_bytes;
+    const uint32_t a0 = s * a.bps;
+    const auto rsrc = make_rsrc(reinterpret_cast<const char*>(gw.trellis) + uint64_t(a0) * row_bytes,
+                                a.bps * row_bytes);
+    const uint32_t lane_off = (8u * c + jt) * tile_bytes + g * 4u * K;
+    const int nb = a.bps / GEMV_WAVES;   // even: bps is a multiple of 8
+    const uint32_t act_row = a.bps * 16;
+
+    _Float16* act = reinterpret_cast<_Float16*>(smem);                  // [RT][bps*16]
+    float* red = reinterpret_cast<float*>(smem + RT * act_row * 2);       // [4][RT][128]
+
+    Chunk<K> c0, c1;
+    load_chunk(c0, rsrc, w * row_bytes + lane_off);
+    load_chunk(c1, rsrc, (w + GEMV_WAVES) * row_bytes + lane_off);
+
+    // Prologue: FP16 core input of this split's channels.
+    const int hblocks = a.bps / 8;
+    for (int u = w; u < RT * hblocks; u += GEMV_WAVES) {
+        const int r = u / hblocks, hb = u % hblocks;
+        const uint32_t ch = a0 * 16 + hb * 128;
+        const bool live = uint32_t(r) < a.rows;
+        input_block(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, act + r * act_row + hb * 128, live);
+    }
+    __syncthreads();
+
+    float acc[RT][2];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+
+    const bool first = g == 0;
+    for (int t = 0; t < nb; t += 2) {
+        link_chunk(c0, first);
+        gemv_block<K, CB, RT>(c0, act + (w + GEMV_WAVES * t) * 16, act_row, acc);
+        if (t + 2 < nb) load_chunk(c0, rsrc, (w + GEMV_WAVES * (t + 2)) * row_bytes + lane_off);
+        link_chunk(c1, first);
+        gemv_block<K, CB, RT>(c1, act + (w + GEMV_WAVES * (t + 1)) * 16, act_row, acc);
+        if (t + 3 < nb) load_chunk(c1, rsrc, (w + GEMV_WAVES * (t + 3)) * row_bytes + lane_off);
+    }
+
+    // Wave partials -> LDS, added in wave order.
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        red[(w * RT + r) * 128 + 16 * jt + g] = acc[r][0];
+        red[(w * RT + r) * 128 + 16 * jt + g + 8] = acc[r][1];
+    }
+    __syncthreads();
+    float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
+    for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
+        const int r = idx >> 7, n = idx & 127;
+        float v = red[(0 * RT + r) * 128 + n];
+#pragma unroll
+        for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + red[(ww * RT + r) * 128 + n];
+        if (a.splits == 1) {
+            red[r * 128 + n] = v;
+        } else if (uint32_t(r) < a.rows) {
+            plane_base[(uint64_t(s) * a.rows + r) * a.N + 128 * c + n] = v;
+        }
+    }
+    if (a.splits == 1) {
+        __syncthreads();
+        finish_columns(a, gw, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
+        return;
+    }
+    if (a.mode == 0) return;
+
+    // Single-launch completion: the last workgroup of column group (z, c) finishes.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    uint32_t* counter = a.counters + uint64_t(z) * (a.N >> 7) + c;
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = old == a.splits - 1;
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    finish_columns(a, gw, y, c, a.splits, [&](int ss, int r) -> const float* {
+        return plane_base + (uint64_t(ss) * a.rows + r) * a.N + 128 * c;
+    });
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Second launch of the two-kernel path: fold + output stage per column group.
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a);
+
+// Decode to FP16 Q[I][N] (diagnostic): grid (N/128, I/16), one wave per 8 tiles.
+template <int K, int CB>
+__global__ __launch_bounds__(64) void decode_kernel(const uint32_t* trellis, uint32_t N, uint64_t bytes,
+                                                    _Float16* q) {
+    const int c = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x;
+    const int jt = lane >> 3, g = lane & 7;
+    constexpr uint32_t tile_bytes = 32u * K;
+    const uint32_t row_bytes = (N >> 4) * tile_bytes;
+    const auto rsrc = make_rsrc(reinterpret_cast<const char*>(trellis) + uint64_t(blk) * row_bytes, row_bytes);
+    Chunk<K> ch;
+    load_chunk(ch, rsrc, (8u * c + jt) * tile_bytes + g * 4u * K);
+    link_chunk(ch, g == 0);
+    half2_t wq[4][4];
+    decode_chunk<K, CB>(ch, wq);
+    const uint64_t col0 = 16u * (8u * c + jt) + g, col1 = col0 + 8;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const uint64_t r0 = 16u * blk + 2 * v, r8 = r0 + 8;
+        q[r0 * N + col0] = wq[v][0].x;
+        q[(r0 + 1) * N + col0] = wq[v][0].y;
+        q[r8 * N + col0] = wq[v][1].x;
+        q[(r8 + 1) * N + col0] = wq[v][1].y;
+        q[r0 * N + col1] = wq[v][2].x;
+        q[(r0 + 1) * N + col1] = wq[v][2].y;
+        q[r8 * N + col1] = wq[v][3].x;
+        q[(r8 + 1) * N + col1] = wq[v][3].y;
+    }
+}
+
+struct GemvLaunch {
+    GemvArgs args;
+    dim3 grid;
+    uint32_t rows_template;   // 1, 2, 4 or 8
+    uint32_t codebook;
+    size_t lds;
+    hipStream_t stream;
+};
+
+template <int K>
+hipError_t gemv_dispatch(const GemvLaunch& l);
+template <int K>
+hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t I, uint32_t N, uint64_t bytes,
+                           _Float16* q, hipStream_t stream);
+
+#define STX_INSTANTIATE_GEMV(K)                                                                           \
+    template <>                                                                                           \
+    hipError_t gemv_dispatch<K>(const GemvLaunch& l) {                                                    \
+        using Fn = void (*)(GemvArgs);                                                                    \
+        static const Fn table[3][4] = {                                                                   \
+            {gemv_kernel<K, 0, 1>, gemv_kernel<K, 0, 2>, gemv_kernel<K, 0, 4>, gemv_kernel<K, 0, 8>},     \
+            {gemv_kernel<K, 1, 1>, gemv_kernel<K, 1, 2>, gemv_kernel<K, 1, 4>, gemv_kernel<K, 1, 8>},     \
+            {gemv_kernel<K, 2, 1>, gemv_kernel<K, 2, 2>, gemv_kernel<K, 2, 4>, gemv_kernel<K, 2, 8>}};    \
+        const int ri = l.rows_template == 1 ? 0 : l.rows_template == 2 ? 1 : l.rows_template == 4 ? 2 : 3; \
+        hipLaunchKernelGGL(table[l.codebook][ri], l.grid, dim3(GEMV_THREADS), l.lds, l.stream, l.args);   \
+        return hipGetLastError();                                                                         \
+    }                                                                                                     \
+    template <>                                                                                           \
+    hipError_t decode_dispatch<K>(uint32_t codebook, const uint32_t* trellis, uint32_t I, uint32_t N,     \
+                                  uint64_t bytes, _Float16* q, hipStream_t stream) {                      \
+        using Fn = void (*)(const uint32_t*, uint32_t, uint64_t, _Float16*);                               \
+        static const Fn table[3] = {decode_kernel<K, 0>, decode_kernel<K, 1>, decode_kernel<K, 2>};       \
+        hipLaunchKernelGGL(table[codebook], dim3(N / 128, I / 16), dim3(64), 0, stream, trellis, N, bytes, q); \
+        return hipGetLastError();                                                                         \
+    }
+
+}  // namespace stx

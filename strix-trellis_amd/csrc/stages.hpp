@@ -1,0 +1,68 @@
+// H128 input and output stages for gfx950 wave64.
+//
+// Arithmetic (reference docs/NUMERICS.md:30-65, python/strix_trellis/linear.py:82-163):
+//   input : a = RN16( H32( f32( RN16( RN32(x * f32(suh)) ) ) ) )
+//   output: y = RN32(H32(core) * f32(svh)) [+ bias] ; y = RN32(y * alpha) ; y = RN32(y + RN32(beta * old)) iff beta != 0
+//   H32   : butterflies of strides 1, 2, ..., 64 in that order, each add/sub
+//           rounded to FP32, then one multiply by RN32(1/sqrt(128)).
+// Every step is a single IEEE FP32 operation (the library is compiled with
+// -ffp-contract=off), so any schedule that performs the same operations on the
+// same pairs gives the same bits.  Here one wave owns one 128-block: lane l
+// holds elements l and l+64; strides 1..32 pair lanes through shuffles, stride
+// 64 pairs the two registers of a lane.
+#pragma once
+#include "trellis.hpp"
+
+namespace stx {
+
+constexpr float INV_SQRT128 = 0x1.6a09e6p-4f;   // RN32(1/sqrt(128))
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+__device__ __forceinline__ void h32_wave(float& v0, float& v1) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int stride = 1; stride < 64; stride <<= 1) {
+        const float p0 = __shfl_xor(v0, stride, 64);
+        const float p1 = __shfl_xor(v1, stride, 64);
+        const bool upper = (lane & stride) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+    const float a = v0, b = v1;
+    v0 = rn32(a + b);
+    v1 = rn32(a - b);
+    v0 = rn32(v0 * INV_SQRT128);
+    v1 = rn32(v1 * INV_SQRT128);
+}
+
+// Input stage of one 128-block: x and suh point at its first channel.  The
+// wave writes the 128 FP16 core inputs to `out` (LDS or global).
+__device__ __forceinline__ void input_block(const float* x, const uint16_t* suh, _Float16* out, bool live) {
+    const int lane = threadIdx.x & 63;
+    float v[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + 64 * h;
+        const float xv = live ? x[i] : 0.0f;
+        const float scaled = rn32(xv * half_bits_to_float(suh[i]));
+        v[h] = (float)(_Float16)scaled;
+    }
+    h32_wave(v[0], v[1]);
+    out[lane] = (_Float16)v[0];
+    out[lane + 64] = (_Float16)v[1];
+}
+
+// Output epilogue for one element after the H32 of its 128-block.
+__device__ __forceinline__ float output_element(float h, uint16_t svh, const float* bias, int n,
+                                                float alpha, float beta, const float* old) {
+    float y = rn32(h * half_bits_to_float(svh));
+    if (bias) y = rn32(y + bias[n]);
+    y = rn32(y * alpha);
+    if (beta != 0.0f) y = rn32(y + rn32(beta * *old));
+    return y;
+}
+
+}  // namespace stx

@@ -1,0 +1,14 @@
+"""strix_trellis for MI355X: EXL3 / QTIP trellis linear layers on gfx950.
+
+The compute path is libstrix_trellis.so (hand-written HIP for gfx950 behind
+the reference's C ABI v1, include/strix_trellis.h).  This package is the thin
+Python host layer over it:
+
+``abi``      ctypes mirror of the C ABI (descriptors, statuses, library loader);
+``runtime``  contexts, prepared weights, GEMV/GEMM calls, plans (torch device buffers).
+"""
+from . import abi
+from .abi import StrixError
+
+__all__ = ["abi", "StrixError"]
+__version__ = "0.3.0"

@@ -1,0 +1,268 @@
+"""Python host layer over the C ABI (ctypes): contexts, prepared weights, calls, plans.
+
+Device buffers are PyTorch-ROCm tensors (``torch`` supplies device memory and
+streams only); every computation runs in libstrix_trellis.so.  Errors surface
+as :class:`abi.StrixError` carrying the C status.
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import abi
+
+_torch = None
+
+
+def _t():
+    global _torch
+    if _torch is None:
+        import torch
+        _torch = torch
+    return _torch
+
+
+def stream_desc(stream=None):
+    """strix_stream for a torch stream (default: torch's current stream)."""
+    torch = _t()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return abi.header(abi.Stream, hip_stream=C.c_void_p(s.cuda_stream or None))
+
+
+def tensor_desc(t, rank=None, width=None):
+    """F32 tensor descriptor of a contiguous torch tensor (rank 1 or 2)."""
+    d = abi.header(abi.TensorDesc)
+    d.dtype = abi.DTYPE_F32
+    if t is None:
+        d.rank = rank or 2
+        d.shape[0] = 0
+        d.shape[1] = width or 0
+        d.strides[0] = width or 0
+        d.strides[1] = 1
+        return d
+    if t.dtype != _t().float32 or not t.is_contiguous():
+        raise ValueError("tensors must be contiguous float32")
+    d.data = C.c_void_p(t.data_ptr() or None)
+    d.buffer_bytes = t.numel() * 4
+    d.rank = t.dim() if rank is None else rank
+    if d.rank == 1:
+        d.shape[0] = t.shape[0]
+        d.strides[0] = 1
+    else:
+        d.shape[0], d.shape[1] = t.shape[0], t.shape[1]
+        d.strides[0], d.strides[1] = t.shape[1], 1
+    return d
+
+
+class Context:
+    def __init__(self, device=0):
+        self.lib = abi.load()
+        desc = abi.header(abi.ContextDesc, device_ordinal=device)
+        h = C.c_void_p()
+        abi.check(self.lib.strix_context_create(C.byref(desc), C.byref(h)), "strix_context_create")
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            abi.check(self.lib.strix_context_destroy(self.handle), "strix_context_destroy")
+            self.handle = None
+
+
+class Weights:
+    """Prepared EXL3 weights (one private device allocation)."""
+
+    def __init__(self, ctx, trellis, suh, svh, bias=None, codebook="mul1", stream=None, blob=False):
+        self.ctx, self.lib = ctx, ctx.lib
+        tr = np.ascontiguousarray(trellis)
+        if tr.ndim != 3 or tr.dtype.itemsize != 2:
+            raise ValueError("trellis must be [I/16, N/16, 16K] 16-bit words")
+        self.input, self.output = tr.shape[0] * 16, tr.shape[1] * 16
+        self.bits = tr.shape[2] // 16
+        self.codebook = codebook
+        self._keep = [tr.view(np.uint16), np.ascontiguousarray(suh, dtype=np.float16),
+                      np.ascontiguousarray(svh, dtype=np.float16),
+                      None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)]
+        h = C.c_void_p()
+        sd = stream_desc(stream)
+        if blob:
+            status = self._prepare_blob(sd, h)
+        else:
+            parts = abi.header(abi.PartsDesc, transport_version=abi.TRANSPORT_VERSION, bits_x2=2 * self.bits,
+                               rows=self.output, columns=self.input, codebook=abi.CODEBOOK[codebook],
+                               marker=abi.MARKER[codebook])
+            for name, arr in zip(("trellis", "suh", "svh", "bias"), self._keep):
+                if arr is not None:
+                    setattr(parts, name, abi.HostRegion(arr.ctypes.data, arr.nbytes))
+            status = self.lib.strix_weights_prepare_parts(ctx.handle, C.byref(parts), C.byref(sd), C.byref(h))
+        abi.check(status, "strix_weights_prepare")
+        self.handle = h
+
+    def _prepare_blob(self, sd, h):
+        tr, suh, svh, bias = self._keep
+        chunks, offsets, pos = [], [], 0
+        for arr in (tr, suh, svh, bias):
+            if arr is None:
+                offsets.append((0, 0))
+                continue
+            pos = (pos + 3) & ~3
+            offsets.append((pos, arr.nbytes))
+            chunks.append((pos, arr))
+            pos += arr.nbytes
+        blob = np.zeros(pos, dtype=np.uint8)
+        for off, arr in chunks:
+            blob[off:off + arr.nbytes] = arr.view(np.uint8).reshape(-1)
+        m = abi.Metadata(struct_size=C.sizeof(abi.Metadata), transport_version=abi.TRANSPORT_VERSION,
+                         rows=self.output, columns=self.input, bits_x2=2 * self.bits,
+                         codebook=abi.CODEBOOK[self.codebook], marker=abi.MARKER[self.codebook])
+        (m.trellis_offset, m.trellis_bytes), (m.suh_offset, m.suh_bytes), (m.svh_offset, m.svh_bytes), \
+            (m.bias_offset, m.bias_bytes) = offsets
+        t = abi.header(abi.TransportDesc, format=abi.TRANSPORT_EXL3_CANONICAL,
+                       transport_version=abi.TRANSPORT_VERSION, data=blob.ctypes.data, data_bytes=blob.nbytes,
+                       metadata=C.addressof(m), metadata_bytes=C.sizeof(m), rows=self.output, columns=self.input)
+        self._blob, self._meta = blob, m
+        return self.lib.strix_weights_prepare(self.ctx.handle, C.byref(t), C.byref(sd), C.byref(h))
+
+    @property
+    def packed_bytes(self):
+        return self.input * self.output * self.bits // 8
+
+    def destroy(self):
+        if self.handle:
+            abi.check(self.lib.strix_weights_destroy(self.handle), "strix_weights_destroy")
+            self.handle = None
+
+    def gemv_shape(self):
+        bps, splits = C.c_uint32(), C.c_uint32()
+        abi.check(self.lib.strix_amd_gemv_shape(self.handle, C.byref(bps), C.byref(splits)))
+        return bps.value, splits.value
+
+    # -- diagnostics -----------------------------------------------------------
+    def decode(self, stream=None):
+        torch = _t()
+        q = torch.empty((self.input, self.output), dtype=torch.float16, device=f"cuda:{self.ctx.device}")
+        abi.check(self.lib.strix_amd_decode(self.handle, C.c_void_p(q.data_ptr()), q.numel() * 2,
+                                            C.byref(stream_desc(stream))), "strix_amd_decode")
+        return q
+
+    def input_stage(self, x, stream=None):
+        torch = _t()
+        x = x.reshape(-1, self.input)
+        a = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+        abi.check(self.lib.strix_amd_input_stage(self.handle, C.c_void_p(x.data_ptr() or None), x.shape[0],
+                                                 C.c_void_p(a.data_ptr() or None), a.numel() * 2,
+                                                 C.byref(stream_desc(stream))), "strix_amd_input_stage")
+        return a
+
+    def output_stage(self, core, y=None, alpha=1.0, beta=0.0, stream=None):
+        torch = _t()
+        core = core.reshape(-1, self.output)
+        if y is None:
+            y = torch.empty(core.shape, dtype=torch.float32, device=core.device)
+        abi.check(self.lib.strix_amd_output_stage(self.handle, C.c_void_p(core.data_ptr() or None), core.shape[0],
+                                                  C.c_void_p(y.data_ptr() or None), y.numel() * 4, alpha, beta,
+                                                  C.byref(stream_desc(stream))), "strix_amd_output_stage")
+        return y
+
+
+def matmul_desc(weights, x, y, alpha=1.0, beta=0.0, workspace=None, rank=None):
+    d = abi.MatmulDesc()
+    weights.lib.strix_matmul_desc_init(C.byref(d))
+    d.weights = weights.handle
+    d.input = tensor_desc(x, rank, weights.input)
+    d.output = tensor_desc(y, rank, weights.output)
+    d.alpha, d.beta = alpha, beta
+    if workspace is not None:
+        d.workspace = C.c_void_p(workspace.data_ptr() or None)
+        d.workspace_bytes = workspace.numel() * workspace.element_size()
+    return d
+
+
+def workspace_bytes(weights, x, y, rank=None):
+    d = matmul_desc(weights, x, y, rank=rank)
+    out = C.c_uint64()
+    abi.check(weights.lib.strix_matmul_workspace_bytes(weights.ctx.handle, C.byref(d), C.byref(out)),
+              "strix_matmul_workspace_bytes")
+    return out.value
+
+
+def alloc_workspace(nbytes, device):
+    torch = _t()
+    # torch's caching allocator returns 512-byte aligned blocks.
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _call(fn, weights, x, y, alpha, beta, workspace, stream, rank):
+    if workspace is None:
+        workspace = alloc_workspace(workspace_bytes(weights, x, y, rank), x.device)
+    d = matmul_desc(weights, x, y, alpha, beta, workspace, rank)
+    abi.check(fn(weights.ctx.handle, C.byref(d), C.byref(stream_desc(stream))), fn.__name__)
+    return y
+
+
+def gemv(weights, x, y, alpha=1.0, beta=0.0, workspace=None, stream=None):
+    return _call(weights.lib.strix_gemv, weights, x, y, alpha, beta, workspace, stream, None)
+
+
+def gemm(weights, x, y, alpha=1.0, beta=0.0, workspace=None, stream=None):
+    return _call(weights.lib.strix_gemm, weights, x, y, alpha, beta, workspace, stream, None)
+
+
+class LinearPlan:
+    def __init__(self, weights, x, y, alpha=1.0, beta=0.0, workspace=None, stream=None, operation="gemv"):
+        self.lib = weights.lib
+        if workspace is None:
+            workspace = alloc_workspace(workspace_bytes(weights, x, y), x.device)
+        self._keep = (weights, x, y, workspace)
+        d = matmul_desc(weights, x, y, alpha, beta, workspace)
+        op = abi.OPERATION_GEMV if operation == "gemv" else abi.OPERATION_GEMM
+        h = C.c_void_p()
+        abi.check(self.lib.strix_linear_plan_create(weights.ctx.handle, C.byref(d), C.byref(stream_desc(stream)), op,
+                                                    C.byref(h)), "strix_linear_plan_create")
+        self.handle = h
+
+    def submit(self):
+        abi.check(self.lib.strix_linear_plan_submit(self.handle), "strix_linear_plan_submit")
+
+    def launches(self):
+        n = C.c_uint32()
+        abi.check(self.lib.strix_amd_plan_launches(self.handle, C.byref(n)))
+        return n.value
+
+    def destroy(self):
+        if self.handle:
+            abi.check(self.lib.strix_linear_plan_destroy(self.handle), "strix_linear_plan_destroy")
+            self.handle = None
+
+
+class GroupedGemvPlan:
+    """Grouped strided GEMV: y[r][g*ogs + n] = Linear_g(x[r][g*igs + i])."""
+
+    def __init__(self, weights_list, x, y, rows, igs, ogs, irs, ors, stream=None, workspace=None):
+        self.lib = weights_list[0].lib
+        ctx = weights_list[0].ctx
+        handles = (C.c_void_p * len(weights_list))(*[w.handle.value for w in weights_list])
+        d = abi.header(abi.GroupedGemvDesc, weights=C.cast(handles, C.POINTER(C.c_void_p)),
+                       group_count=len(weights_list), rows=rows, flags=abi.GEMV_ROW_INVARIANT_R1,
+                       input=C.c_void_p(x.data_ptr()), input_row_stride=irs, input_group_stride=igs,
+                       input_buffer_bytes=x.numel() * 4, output=C.c_void_p(y.data_ptr()),
+                       output_row_stride=ors, output_group_stride=ogs, output_buffer_bytes=y.numel() * 4)
+        need = C.c_uint64()
+        abi.check(self.lib.strix_grouped_gemv_workspace_bytes(ctx.handle, C.byref(d), C.byref(need)),
+                  "strix_grouped_gemv_workspace_bytes")
+        if workspace is None:
+            workspace = alloc_workspace(need.value, x.device)
+        d.workspace = C.c_void_p(workspace.data_ptr())
+        d.workspace_bytes = workspace.numel()
+        self._keep = (weights_list, x, y, workspace, handles)
+        h = C.c_void_p()
+        abi.check(self.lib.strix_grouped_gemv_plan_create(ctx.handle, C.byref(d), C.byref(stream_desc(stream)),
+                                                          C.byref(h)), "strix_grouped_gemv_plan_create")
+        self.handle = h
+
+    def submit(self):
+        abi.check(self.lib.strix_grouped_gemv_plan_submit(self.handle), "strix_grouped_gemv_plan_submit")
+
+    def destroy(self):
+        if self.handle:
+            abi.check(self.lib.strix_grouped_gemv_plan_destroy(self.handle), "strix_grouped_gemv_plan_destroy")
+            self.handle = None
