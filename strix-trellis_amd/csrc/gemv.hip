@@ -6,12 +6,14 @@ namespace stx {
 
 // Split decomposition.  The whole matrix must be in flight at once for the
 // small decode shapes (8 MiB at K4 4096^2 is about one HBM latency-bandwidth
-// product), so aim for >= 1024 workgroups of 4 waves; among candidate splits
-// (bps = 8m with m dividing (I/16)/8, m <= 16) take the largest bps that keeps
-// the grid at or above that target, else the smallest bps.
+// product), so aim for >= 512 workgroups of 4 waves (measured on MI355X:
+// 1024 adds more cross-workgroup fold traffic than it hides, 256 leaves SIMDs
+// idle); among candidate splits (bps = 8m with m dividing (I/16)/8, m <= 16)
+// take the largest bps that keeps the grid at or above that target, else the
+// smallest bps.
 GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t /*bits*/) {
     const uint32_t nb = input / 16, nc = output / 128, units = nb / 8;
-    constexpr uint32_t target = 1024;
+    constexpr uint32_t target = 512;
     GemvShape best{8, nb / 8};
     for (uint32_t m = 1; m <= 16; ++m) {
         if (units % m) continue;
@@ -46,7 +48,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
     const GroupWeights gw = group_weights(a, z);
     float* y = a.y + z * a.y_group_stride;
     const float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
-    finish_columns(a, gw, y, c, a.splits, [&](int s, int r) -> const float* {
+    finish_columns<true>(a, gw, y, c, a.splits, [&](int s, int r) -> const float* {
         return plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c;
     });
 }
@@ -83,7 +85,15 @@ static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table,
     return l;
 }
 
+// The per-split buffer resource spans bps rows of tiles and must stay below
+// 2^31 bytes (its out-of-range sentinel); the split count is a grid dimension.
+static bool gemv_fits(const DeviceWeights& w) {
+    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
+    return uint64_t(sh.bps) * (w.output / 16) * 32u * w.bits < (uint64_t(1) << 31) && sh.splits <= 65535;
+}
+
 hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream) {
+    if (!gemv_fits(w)) return hipErrorInvalidValue;
     GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, nullptr, 0, stream);
     hipError_t e = gemv_table[w.bits - 1](l);
     if (e != hipSuccess || l.args.splits == 1) return e;
@@ -93,6 +103,7 @@ hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream
 
 hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, uint32_t* counters,
                              hipStream_t stream) {
+    if (!gemv_fits(w)) return hipErrorInvalidValue;
     GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, counters, 1, stream);
     return gemv_table[w.bits - 1](l);
 }
@@ -100,6 +111,7 @@ hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, uin
 hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
                                const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
                                uint32_t* counters, hipStream_t stream) {
+    if (!gemv_fits(geometry)) return hipErrorInvalidValue;
     GemvLaunch l = make_launch(geometry, table, groups, call, x_group_stride, y_group_stride, counters,
                                counters ? 1 : 0, stream);
     hipError_t e = gemv_table[geometry.bits - 1](l);

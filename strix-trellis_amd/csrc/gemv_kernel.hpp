@@ -55,34 +55,80 @@ __device__ __forceinline__ GroupWeights group_weights(const GemvArgs& a, int z) 
     return a.table ? a.table[z] : a.w;
 }
 
+// Partial planes cross workgroups (and XCDs, each with its own L2), so they
+// are written and read with agent-scope coherent accesses (sc1): completed
+// stores are visible device-wide without the full-L2 writeback an agent-scope
+// release fence costs.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Output stage of column group c for every row: fold, H32, epilogue.
 // `plane(s, r)` returns the pointer to the 128 values of split s, row r.
-template <typename Plane>
+template <bool COHERENT, typename Plane>
 __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWeights& gw, float* y, int c,
                                                int splits, Plane plane) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    auto load = [](const float* p) -> float {
+        if constexpr (COHERENT) return load_coherent(p);
+        else return *p;
+    };
     for (uint32_t r = w; r < a.rows; r += GEMV_WAVES) {
         float z0 = 0.0f, z1 = 0.0f;
-        for (int s = 0; s < splits; ++s) {
+        int s = 0;
+        // Issue a batch of loads before the (ordered) adds that consume them:
+        // one memory round trip per 32 splits.
+        for (; s + 32 <= splits; s += 32) {
+            float v0[32], v1[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) {
+                const float* p = plane(s + u, r);
+                v0[u] = load(p + lane);
+                v1[u] = load(p + lane + 64);
+            }
+#pragma unroll
+            for (int u = 0; u < 32; ++u) {
+                z0 = z0 + v0[u];
+                z1 = z1 + v1[u];
+            }
+        }
+        for (; s + 8 <= splits; s += 8) {
+            float v0[8], v1[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float* p = plane(s + u, r);
+                v0[u] = load(p + lane);
+                v1[u] = load(p + lane + 64);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                z0 = z0 + v0[u];
+                z1 = z1 + v1[u];
+            }
+        }
+        for (; s < splits; ++s) {
             const float* p = plane(s, r);
-            z0 = z0 + p[lane];
-            z1 = z1 + p[lane + 64];
+            z0 = z0 + load(p + lane);
+            z1 = z1 + load(p + lane + 64);
         }
         h32_wave(z0, z1);
         const int n0 = 128 * c + lane, n1 = n0 + 64;
         float* yr = y + r * a.y_row_stride;
-        const float o0 = output_element(z0, gw.svh[n0], gw.bias, n0, a.alpha, a.beta, yr + n0);
-        const float o1 = output_element(z1, gw.svh[n1], gw.bias, n1, a.alpha, a.beta, yr + n1);
-        yr[n0] = o0;
-        yr[n1] = o1;
+        const float o0 = output_element(z0, ld_global(gw.svh + n0), gw.bias, n0, a.alpha, a.beta, yr + n0);
+        const float o1 = output_element(z1, ld_global(gw.svh + n1), gw.bias, n1, a.alpha, a.beta, yr + n1);
+        *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+        *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
     }
 }
 
-template <int K, int CB, int RT>
-__device__ __forceinline__ void gemv_block(const Chunk<K>& chunk, const _Float16* act, uint32_t act_row,
-                                           float (&acc)[RT][2]) {
-    half2_t wq[4][4];
-    decode_chunk<K, CB>(chunk, wq);
+// Dot of one decoded chunk (32 weights: columns g and g+8, rows 0..15 of one
+// input block) with the block's FP16 activations of every row.
+template <int RT>
+__device__ __forceinline__ void dot_block(const half2_t (&wq)[4][4], const _Float16* act, uint32_t act_row,
+                                          float (&acc)[RT][2]) {
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         const u32x4* p = reinterpret_cast<const u32x4*>(act + r * act_row);
@@ -125,32 +171,71 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     _Float16* act = reinterpret_cast<_Float16*>(smem);                  // [RT][bps*16]
     float* red = reinterpret_cast<float*>(smem + RT * act_row * 2);       // [4][RT][128]
 
-    Chunk<K> c0, c1;
-    load_chunk(c0, rsrc, w * row_bytes + lane_off);
-    load_chunk(c1, rsrc, (w + GEMV_WAVES) * row_bytes + lane_off);
-
-    // Prologue: FP16 core input of this split's channels.
-    const int hblocks = a.bps / 8;
-    for (int u = w; u < RT * hblocks; u += GEMV_WAVES) {
+    // Prefetch ring of depth 4.  Loads are issued unconditionally so the
+    // compiler can count them exactly (vmcnt(3) per use); past the last block
+    // the offset is out of the buffer's range, which the hardware answers
+    // with zeros and no memory access.
+    constexpr uint32_t kOutOfRange = 0x80000000u;
+    auto block_off = [&](int t) -> uint32_t {
+        return t < nb ? (w + GEMV_WAVES * t) * row_bytes + lane_off : kOutOfRange;
+    };
+    // Prologue: FP16 core input of this split's channels, one 128-block unit
+    // per wave.  The first two units' loads are issued before the weight
+    // prefetch, so waiting for them does not wait for the weights.
+    const int hblocks = a.bps / 8, units = RT * hblocks;
+    auto unit_load = [&](int u) -> InputLoad {
         const int r = u / hblocks, hb = u % hblocks;
         const uint32_t ch = a0 * 16 + hb * 128;
         const bool live = uint32_t(r) < a.rows;
-        input_block(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, act + r * act_row + hb * 128, live);
-    }
+        return input_load(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, live);
+    };
+    auto unit_out = [&](int u) -> _Float16* { return act + (u / hblocks) * act_row + (u % hblocks) * 128; };
+    // Units past the end load unit 0 again (valid addresses, result unused).
+    const InputLoad pre0 = unit_load(w < units ? w : 0);
+    const InputLoad pre1 = unit_load(w + GEMV_WAVES < units ? w + GEMV_WAVES : 0);
+    __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the weight prefetch
+
+    Chunk<K> ring[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_chunk(ring[u], rsrc, block_off(u));
+
+    // Decode the first two blocks before the prologue's arithmetic and barrier:
+    // this VALU work overlaps the latency of the input-stage loads (which
+    // queue behind the weight traffic of the whole grid) and of the other
+    // waves' H128 shuffles.  Their slots are refilled with blocks 4 and 5.
+    const bool first = g == 0;
+    half2_t d0[4][4], d1[4][4];
+    link_chunk(ring[0], first);
+    decode_chunk<K, CB>(ring[0], d0);
+    load_chunk(ring[0], rsrc, block_off(4));
+    link_chunk(ring[1], first);
+    decode_chunk<K, CB>(ring[1], d1);   // nb >= 2 always
+    load_chunk(ring[1], rsrc, block_off(5));
+
+    if (w < units) input_compute(pre0, unit_out(w));
+    if (w + GEMV_WAVES < units) input_compute(pre1, unit_out(w + GEMV_WAVES));
+    for (int u = w + 2 * GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
     __syncthreads();
 
     float acc[RT][2];
 #pragma unroll
     for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+    dot_block<RT>(d0, act + w * 16, act_row, acc);
+    dot_block<RT>(d1, act + (w + GEMV_WAVES) * 16, act_row, acc);
 
-    const bool first = g == 0;
-    for (int t = 0; t < nb; t += 2) {
-        link_chunk(c0, first);
-        gemv_block<K, CB, RT>(c0, act + (w + GEMV_WAVES * t) * 16, act_row, acc);
-        if (t + 2 < nb) load_chunk(c0, rsrc, (w + GEMV_WAVES * (t + 2)) * row_bytes + lane_off);
-        link_chunk(c1, first);
-        gemv_block<K, CB, RT>(c1, act + (w + GEMV_WAVES * (t + 1)) * 16, act_row, acc);
-        if (t + 3 < nb) load_chunk(c1, rsrc, (w + GEMV_WAVES * (t + 3)) * row_bytes + lane_off);
+    // Blocks t >= 2: slot (t + 2) % 4 holds block t; it is refilled with block t + 4.
+    for (int t = 2; t < nb; t += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            Chunk<K>& slot = ring[(u + 2) & 3];
+            if (t + u < nb) {
+                half2_t wq[4][4];
+                link_chunk(slot, first);
+                decode_chunk<K, CB>(slot, wq);
+                dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+            }
+            load_chunk(slot, rsrc, block_off(t + u + 4));
+        }
     }
 
     // Wave partials -> LDS, added in wave order.
@@ -169,28 +254,31 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
         if (a.splits == 1) {
             red[r * 128 + n] = v;
         } else if (uint32_t(r) < a.rows) {
-            plane_base[(uint64_t(s) * a.rows + r) * a.N + 128 * c + n] = v;
+            store_coherent(plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c + n, v);
         }
     }
     if (a.splits == 1) {
         __syncthreads();
-        finish_columns(a, gw, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
+        finish_columns<false>(a, gw, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
         return;
     }
     if (a.mode == 0) return;
 
-    // Single-launch completion: the last workgroup of column group (z, c) finishes.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // Single-launch completion: the last workgroup of column group (z, c)
+    // finishes.  The coherent stores above are complete (waitcnt) before the
+    // counter increment; the finishing loads are issued after it returned.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     uint32_t* counter = a.counters + uint64_t(z) * (a.N >> 7) + c;
     if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last_flag = old == a.splits - 1;
     }
     __syncthreads();
     if (!last_flag) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    finish_columns(a, gw, y, c, a.splits, [&](int ss, int r) -> const float* {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    finish_columns<true>(a, gw, y, c, a.splits, [&](int ss, int r) -> const float* {
         return plane_base + (uint64_t(ss) * a.rows + r) * a.N + 128 * c;
     });
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

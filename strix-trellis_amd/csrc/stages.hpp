@@ -38,30 +38,49 @@ __device__ __forceinline__ void h32_wave(float& v0, float& v1) {
     v1 = rn32(v1 * INV_SQRT128);
 }
 
-// Input stage of one 128-block: x and suh point at its first channel.  The
-// wave writes the 128 FP16 core inputs to `out` (LDS or global).
-__device__ __forceinline__ void input_block(const float* x, const uint16_t* suh, _Float16* out, bool live) {
+// Input stage of one 128-block, split into the loads and the arithmetic so a
+// kernel can issue the loads ahead of other memory traffic.  x and suh point
+// at the block's first channel; a dead row (live = false) reads nothing and
+// produces zeros.
+struct InputLoad {
+    float x0, x1;
+    uint16_t u0, u1;
+};
+
+__device__ __forceinline__ InputLoad input_load(const float* x, const uint16_t* suh, bool live) {
+    // Branch-free: a dead row still loads (from a valid address) and is zeroed
+    // afterwards, so the loads stay in one basic block with their issuers.
     const int lane = threadIdx.x & 63;
-    float v[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int i = lane + 64 * h;
-        const float xv = live ? x[i] : 0.0f;
-        const float scaled = rn32(xv * half_bits_to_float(suh[i]));
-        v[h] = (float)(_Float16)scaled;
-    }
-    h32_wave(v[0], v[1]);
-    out[lane] = (_Float16)v[0];
-    out[lane + 64] = (_Float16)v[1];
+    InputLoad l;
+    const float a = ld_global(x + lane), b = ld_global(x + lane + 64);
+    l.x0 = live ? a : 0.0f;
+    l.x1 = live ? b : 0.0f;
+    l.u0 = ld_global(suh + lane);
+    l.u1 = ld_global(suh + lane + 64);
+    return l;
+}
+
+// The wave writes the 128 FP16 core inputs to `out` (LDS or global).
+__device__ __forceinline__ void input_compute(const InputLoad& l, _Float16* out) {
+    const int lane = threadIdx.x & 63;
+    float v0 = (float)(_Float16)rn32(l.x0 * half_bits_to_float(l.u0));
+    float v1 = (float)(_Float16)rn32(l.x1 * half_bits_to_float(l.u1));
+    h32_wave(v0, v1);
+    out[lane] = (_Float16)v0;
+    out[lane + 64] = (_Float16)v1;
+}
+
+__device__ __forceinline__ void input_block(const float* x, const uint16_t* suh, _Float16* out, bool live) {
+    input_compute(input_load(x, suh, live), out);
 }
 
 // Output epilogue for one element after the H32 of its 128-block.
 __device__ __forceinline__ float output_element(float h, uint16_t svh, const float* bias, int n,
                                                 float alpha, float beta, const float* old) {
     float y = rn32(h * half_bits_to_float(svh));
-    if (bias) y = rn32(y + bias[n]);
+    if (bias) y = rn32(y + ld_global(bias + n));
     y = rn32(y * alpha);
-    if (beta != 0.0f) y = rn32(y + rn32(beta * *old));
+    if (beta != 0.0f) y = rn32(y + rn32(beta * ld_global(old)));
     return y;
 }
 

@@ -35,6 +35,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// Load through a global-address-space pointer.  Pointers that arrive through
+// structs are generic to the compiler, which would emit FLAT loads; those
+// count on both vmcnt and lgkmcnt and force full waits.
+template <class T>
+__device__ __forceinline__ T ld_global(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)(p);
+}
+
 // Keep an FP32 value in a register so that a later FP32->FP16 conversion is a
 // separate rounding (stops LLVM from forming mixed-precision ops that round
 // once from the wider value).

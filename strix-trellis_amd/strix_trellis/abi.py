@@ -6,6 +6,7 @@ in-tree libstrix_trellis.so built by ``strix-trellis_amd/build.py`` and raises
 if it is missing: there is no fallback implementation.
 """
 import ctypes as C
+import os
 from pathlib import Path
 
 ABI_VERSION = 1
@@ -173,7 +174,8 @@ def load(path=None):
     global _lib
     if _lib is not None and path is None:
         return _lib
-    p = Path(path) if path else LIB_PATH
+    # STRIX_TRELLIS_LIB selects another build of the same library (a path to a .so).
+    p = Path(path) if path else Path(os.environ.get("STRIX_TRELLIS_LIB", LIB_PATH))
     if not p.exists():
         raise RuntimeError(f"libstrix_trellis.so not built at {p}; run strix-trellis_amd/build.py")
     lib = C.CDLL(str(p))
