@@ -33,14 +33,16 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-class GemvRotation:
-    """Distinct device copies of one layer, each with its own single-launch plan.
+class Rotation:
+    """Distinct device copies of one layer, each with its own prepared plan.
 
-    One pass over the copies is captured into a HIP graph (one kernel node per
-    call) so that the timed region measures the GPU, not Python's launch rate.
+    One pass over the copies is captured into a HIP graph (one plan submission
+    per copy) so that the timed region measures the GPU, not Python's launch
+    rate.  The copies share x, y and the workspace (their calls are ordered on
+    one stream).
     """
 
-    def __init__(self, ctx, I, N, K, R, seed, min_bytes=ROTATION_BYTES):
+    def __init__(self, ctx, I, N, K, R, seed, op="gemv", min_bytes=ROTATION_BYTES):
         import torch
         import synth
         from strix_trellis import runtime
@@ -50,13 +52,16 @@ class GemvRotation:
         self.packed = packed
         self.stream = torch.cuda.Stream()
         self.x = torch.from_numpy(synth.activations(R, I, seed + 1)).to("cuda:0")
-        self.weights, self.plans, self.ys = [], [], []
+        self.y = torch.empty((R, N), device="cuda:0")
+        self.weights, self.plans = [], []
+        ws = None
         for _ in range(self.copies):
             w = runtime.Weights(ctx, tr, suh, svh, None, "mul1")
-            y = torch.empty((R, N), device="cuda:0")
+            if ws is None:
+                ws = runtime.alloc_workspace(runtime.workspace_bytes(w, self.x, self.y), "cuda:0")
             self.weights.append(w)
-            self.ys.append(y)
-            self.plans.append(runtime.LinearPlan(w, self.x, y, stream=self.stream))
+            self.plans.append(runtime.LinearPlan(w, self.x, self.y, workspace=ws, stream=self.stream, operation=op))
+        self.workspace = ws
         self.launches = self.plans[0].launches()
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
@@ -94,7 +99,7 @@ def time_steps(run, steps, warmup, stream):
 
 
 def bench_gemv(ctx, I, N, K, R, steps, warmup, seed):
-    rot = GemvRotation(ctx, I, N, K, R, seed)
+    rot = Rotation(ctx, I, N, K, R, seed, "gemv")
     try:
         ms, steps = time_steps(rot.run, steps, warmup, rot.stream)
     finally:
@@ -103,6 +108,18 @@ def bench_gemv(ctx, I, N, K, R, steps, warmup, seed):
     gbps = rot.packed / (ms * 1e-3) / 1e9
     return {"I": I, "N": N, "K": K, "R": R, "us": round(us, 3), "packed_GBps": round(gbps, 1),
             "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "launches": rot.launches,
+            "rotation_copies": rot.copies, "timed_steps": steps}
+
+
+def bench_gemm(ctx, M, I, N, K, steps, warmup, seed):
+    rot = Rotation(ctx, I, N, K, M, seed, "gemm", min_bytes=ROTATION_BYTES // 4)
+    try:
+        ms, steps = time_steps(rot.run, steps, warmup, rot.stream)
+    finally:
+        rot.close()
+    tflops = 2.0 * M * I * N / (ms * 1e-3) / 1e12
+    return {"M": M, "I": I, "N": N, "K": K, "us": round(ms * 1e3, 2), "TFLOPs": round(tflops, 1),
+            "pct_fp16_peak": round(100 * tflops / FP16_PEAK_TFLOPS, 1), "launches": rot.launches,
             "rotation_copies": rot.copies, "timed_steps": steps}
 
 

@@ -7,14 +7,6 @@
 
 namespace stx {
 
-static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
-
-uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
-    // FP16 core input [rows][I] for the MFMA core.
-    if (rows > (UINT64_MAX / 4) / w.input) return UINT64_MAX;
-    return align256(rows * w.input * 2);
-}
-
 uint64_t linear_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
     const uint64_t gemm = gemm_workspace_bytes(w, rows);
     if (gemm == UINT64_MAX) return UINT64_MAX;

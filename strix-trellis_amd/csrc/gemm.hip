@@ -1,10 +1,97 @@
-// Prefill GEMM (rows > 8 or the GEMM entry point).
-#include "backend.hpp"
+// Host side of the prefill GEMM and the fragment-order input stage.
+#include "gemm_wide.hpp"
 
 namespace stx {
 
-uint32_t gemm_launch_count(const DeviceWeights&, uint64_t rows) { return rows ? 2 : 0; }
+__global__ __launch_bounds__(64) void input_stage_frag_kernel(const float* x, const uint16_t* suh, uint32_t M,
+                                                              uint32_t I, _Float16* afrag) {
+    const uint32_t blk = blockIdx.x, row = blockIdx.y;
+    const int lane = threadIdx.x;
+    const bool live = row < M;
+    const uint32_t ch = blk * 128;
+    const InputLoad l = input_load(x + (live ? uint64_t(row) * I : 0) + ch, suh + ch, live);
+    _Float16 v[2];
+    input_values(l, v[0], v[1]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t k = ch + lane + 64 * h;
+        const uint32_t kb32 = k / 32, kk = k % 32;
+        const uint32_t fl = (row % 16) + 16 * (kk / 8);
+        afrag[afrag_offset(row / 16, kb32, I, fl) / 2 + (kk % 8)] = v[h];
+    }
+}
 
-hipError_t launch_gemm(const DeviceWeights&, const LinearCall&, hipStream_t) { return hipErrorNotSupported; }
+// Rows per GEMM pass: the fragment buffer of one pass stays below 1 GiB so
+// its buffer resource (32-bit range) and the workspace stay bounded.
+static uint64_t gemm_pass_rows(const DeviceWeights& w) {
+    const uint64_t per_row = uint64_t(w.input) * 2;
+    uint64_t rows = (uint64_t(1) << 30) / per_row;
+    rows -= rows % 256;
+    return rows < 256 ? 256 : rows;
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+
+uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
+    const uint64_t pass = gemm_pass_rows(w);
+    const uint64_t r = rows < pass ? rows : pass;
+    return align256(((r + 15) / 16) * 16 * w.input * 2);
+}
+
+uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows) {
+    if (!rows) return 0;
+    const uint64_t pass = gemm_pass_rows(w);
+    return uint32_t(2 * ((rows + pass - 1) / pass));
+}
+
+using GemmDispatch = hipError_t (*)(const GemmLaunch&);
+static const GemmDispatch gemm_table[8] = {gemm_dispatch<1>, gemm_dispatch<2>, gemm_dispatch<3>, gemm_dispatch<4>,
+                                           gemm_dispatch<5>, gemm_dispatch<6>, gemm_dispatch<7>, gemm_dispatch<8>};
+static const GemmDispatch gemm_wide_table[8] = {gemm_wide_dispatch<1>, gemm_wide_dispatch<2>, gemm_wide_dispatch<3>,
+                                                gemm_wide_dispatch<4>, gemm_wide_dispatch<5>, gemm_wide_dispatch<6>,
+                                                gemm_wide_dispatch<7>, gemm_wide_dispatch<8>};
+
+// Row-block height: 256 halves the decode work per flop; 128 when the rows
+// would not fill a 256 block or when 256-row blocks leave most CUs idle.
+static uint32_t gemm_bm(uint64_t rows, uint32_t groups) {
+    if (rows <= 128) return 128;
+    const uint64_t wg256 = uint64_t(groups) * ((rows + 255) / 256);
+    return wg256 >= 256 ? 256 : 128;
+}
+
+hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream_t stream) {
+    if (uint64_t(w.input / 16) * (w.output / 16) * 32u * w.bits >= (uint64_t(1) << 31)) return hipErrorInvalidValue;
+    const uint64_t pass = gemm_pass_rows(w);
+    _Float16* afrag = static_cast<_Float16*>(call.workspace);
+    for (uint64_t r0 = 0; r0 < call.rows; r0 += pass) {
+        const uint64_t m = call.rows - r0 < pass ? call.rows - r0 : pass;
+        const uint64_t mpad = (m + 15) / 16 * 16;
+        const float* x = call.x + r0 * call.x_row_stride;
+        hipLaunchKernelGGL(input_stage_frag_kernel, dim3(w.input / 128, uint32_t(mpad)), dim3(64), 0, stream, x,
+                           w.suh, uint32_t(m), w.input, afrag);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        GemmLaunch l{};
+        l.args.trellis = w.trellis;
+        l.args.svh = w.svh;
+        l.args.bias = w.bias;
+        l.args.afrag = afrag;
+        l.args.afrag_bytes = mpad * w.input * 2;
+        l.args.y = call.y + r0 * call.y_row_stride;
+        l.args.M = uint32_t(m);
+        l.args.I = w.input;
+        l.args.N = w.output;
+        l.args.alpha = call.alpha;
+        l.args.beta = call.beta;
+        l.codebook = w.codebook;
+        l.bm = gemm_bm(m, w.output / 128);
+        l.stream = stream;
+        // 256 x 256 tiles once the rows fill them (and N splits into 256-column blocks).
+        const bool wide = m >= 256 && w.output % 256 == 0;
+        e = wide ? gemm_wide_table[w.bits - 1](l) : gemm_table[w.bits - 1](l);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
 
 }  // namespace stx

@@ -61,13 +61,21 @@ __device__ __forceinline__ InputLoad input_load(const float* x, const uint16_t* 
 }
 
 // The wave writes the 128 FP16 core inputs to `out` (LDS or global).
-__device__ __forceinline__ void input_compute(const InputLoad& l, _Float16* out) {
-    const int lane = threadIdx.x & 63;
+// Core inputs of elements lane and lane+64 of the block.
+__device__ __forceinline__ void input_values(const InputLoad& l, _Float16& o0, _Float16& o1) {
     float v0 = (float)(_Float16)rn32(l.x0 * half_bits_to_float(l.u0));
     float v1 = (float)(_Float16)rn32(l.x1 * half_bits_to_float(l.u1));
     h32_wave(v0, v1);
-    out[lane] = (_Float16)v0;
-    out[lane + 64] = (_Float16)v1;
+    o0 = (_Float16)v0;
+    o1 = (_Float16)v1;
+}
+
+__device__ __forceinline__ void input_compute(const InputLoad& l, _Float16* out) {
+    const int lane = threadIdx.x & 63;
+    _Float16 o0, o1;
+    input_values(l, o0, o1);
+    out[lane] = o0;
+    out[lane + 64] = o1;
 }
 
 __device__ __forceinline__ void input_block(const float* x, const uint16_t* suh, _Float16* out, bool live) {

@@ -229,6 +229,17 @@ __device__ __forceinline__ void decode_chunk(const Chunk<K>& c, half2_t (&w)[4][
 #undef STX_DECODE_V
 }
 
+// Pair q (0..15) of decode_chunk: w[q / 4][q % 4] (runtime-unrolled callers
+// pass a constant q).
+template <int K, int CB>
+__device__ __forceinline__ void decode_pair_at(const Chunk<K>& c, half2_t (&w)[4][4], int q) {
+#define STX_PAIR(Q) \
+    if (q == Q) w[Q / 4][Q % 4] = decode_pair<K, CB, Q / 4, 2 * (Q % 4)>(c);
+    STX_PAIR(0) STX_PAIR(1) STX_PAIR(2) STX_PAIR(3) STX_PAIR(4) STX_PAIR(5) STX_PAIR(6) STX_PAIR(7)
+    STX_PAIR(8) STX_PAIR(9) STX_PAIR(10) STX_PAIR(11) STX_PAIR(12) STX_PAIR(13) STX_PAIR(14) STX_PAIR(15)
+#undef STX_PAIR
+}
+
 // Bytes of one tile and of one 16-row block of tiles.
 template <int K>
 struct Geometry {

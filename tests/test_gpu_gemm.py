@@ -1,0 +1,104 @@
+"""GPU parity of the MFMA prefill GEMM (strix_gemm / GEMM plans) through the C ABI.
+
+Bars: the full operator meets the reference GPU gate against the oracle's
+staged FP32 layer (reference docs/GPU_TESTS.md:124-143); the core is within
+max-rel-err 1e-3 of the FP64 product of the same FP16 operands; every row's
+bits are independent of how many rows are submitted with it.
+"""
+import numpy as np
+import pytest
+
+import synth
+from oracle import codec, linear
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from strix_trellis import runtime  # noqa: E402
+
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    c = runtime.Context(0)
+    yield c
+    torch.cuda.synchronize()
+
+
+GEMM_CASES = [
+    # (M, I, N, K, codebook, bias)
+    (16, 256, 256, 4, "mul1", False),
+    (129, 512, 384, 5, "mul1", True),
+    (300, 256, 640, 6, "mul1", False),
+    (512, 1024, 256, 4, "mul1", True),
+    (64, 384, 256, 3, "mcg", False),
+    (40, 256, 128, 2, "3inst", True),
+    (33, 128, 256, 8, "mul1", False),
+    (260, 768, 512, 1, "mul1", False),
+]
+
+
+@pytest.mark.parametrize("M,I,N,K,codebook,bias", GEMM_CASES)
+def test_gemm_matches_oracle(ctx, M, I, N, K, codebook, bias):
+    print(f"gemm M={M} {I}x{N} K={K} {codebook} bias={bias}", flush=True)
+    tr, suh, svh, b = synth.layer(I, N, K, 3000 + M + K, bias)
+    w = runtime.Weights(ctx, tr, suh, svh, b, codebook)
+    x = synth.activations(M, I, 91)
+    y = torch.full((M, N), float("nan"), device=DEV)
+    runtime.gemm(w, torch.from_numpy(x).to(DEV), y)
+    torch.cuda.synchronize()
+    q = codec.dequantize_rotated(tr, K, codebook)
+    ref = linear.matmul_fp32_stages(x, tr, suh, svh, K, codebook, b, rotated=q)["output_fp32"]
+    synth.gate(y.cpu().numpy(), ref)
+    w.destroy()
+
+
+def test_gemm_core_within_fp64_tolerance(ctx):
+    M, I, N, K = 256, 2048, 512, 4
+    tr, _, _, _ = synth.layer(I, N, K, 41)
+    suh = np.ones(I, np.float16)
+    svh = np.ones(N, np.float16)
+    w = runtime.Weights(ctx, tr, suh, svh, None, "mul1")
+    x = synth.activations(M, I, 42)
+    y = torch.empty((M, N), device=DEV)
+    runtime.gemm(w, torch.from_numpy(x).to(DEV), y)
+    got = y.cpu().numpy().astype(np.float64)
+    a = linear.input_stages_fp32(x, suh)["core_input_fp16"].astype(np.float64)
+    exact = a @ codec.dequantize_rotated(tr, K).astype(np.float64)
+    rel = np.max(np.abs(linear.hadamard(got) - exact)) / np.max(np.abs(exact))
+    assert rel <= 1e-3, rel
+    w.destroy()
+
+
+def test_gemm_rows_independent_of_batch_and_alpha_beta(ctx):
+    I, N, K = 512, 512, 5
+    tr, suh, svh, b = synth.layer(I, N, K, 77, bias=True)
+    w = runtime.Weights(ctx, tr, suh, svh, b, "mul1")
+    x = torch.from_numpy(synth.activations(300, I, 78)).to(DEV)
+    y_all = torch.empty((300, N), device=DEV)
+    runtime.gemm(w, x, y_all)
+    y16 = torch.empty((16, N), device=DEV)
+    runtime.gemm(w, x[:16].contiguous(), y16)
+    assert torch.equal(y16.view(torch.int32), y_all[:16].view(torch.int32))
+    y1 = torch.empty((1, N), device=DEV)
+    runtime.gemm(w, x[299:300].contiguous(), y1)
+    assert torch.equal(y1.view(torch.int32), y_all[299:300].view(torch.int32))
+    # alpha / beta epilogue on top of the same core
+    old = torch.from_numpy(synth.rng(5).standard_normal((300, N)).astype(np.float32)).to(DEV)
+    y_ab = old.clone()
+    runtime.gemm(w, x, y_ab, alpha=-0.5, beta=2.0)
+    ref = linear.apply_alpha_beta(y_all.cpu().numpy(), old.cpu().numpy(), -0.5, 2.0)
+    np.testing.assert_array_equal(y_ab.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    # a GEMM plan replays the same bits
+    yp = torch.empty((300, N), device=DEV)
+    plan = runtime.LinearPlan(w, x, yp, operation="gemm")
+    for _ in range(2):
+        yp.fill_(float("nan"))
+        plan.submit()
+        torch.cuda.synchronize()
+        assert torch.equal(yp.view(torch.int32), y_all.view(torch.int32))
+    plan.destroy()
+    w.destroy()
