@@ -3,17 +3,27 @@
 Headline (`value`): decode GEMV, R = 1, K4 mul1, I = N = 4096 (the north-star
 configuration), through a prepared single-launch plan, as packed-weight GB/s
 over a cold rotation of >= 1 GiB of distinct weight copies (more than 4x the
-256 MB MALL), inputs resident in HBM.  One step = one GEMV call.
+256 MB MALL), inputs resident in HBM.  One step = one GEMV call = one launch.
 
-Also reported (same JSON line): the decode GEMV sweep of BASELINE configs[1]
-(R = 1, 2, 4, 8 x {5120^2, 4096 -> 12288} x K4-6), `roofline` for the GEMV
-kernel and `cpu_baseline` (the NumPy oracle on the host, bounded sample).
+Also reported on the same JSON line:
+  sweep_gemv     decode GEMV, R = 1, 2, 4, 8 x {5120^2, 4096 -> 12288} x K4-6
+  sweep_gemm     prefill GEMM, M = 128, 512, 2048 x the same shapes x K4-6
+  grouped_o_a    16 groups x (4096 -> 1024) K5, R = 1..8, one grouped plan
+  roofline       the headline kernel: packed bytes / its mean launch time
+  cpu_baseline   the NumPy oracle on the host cores, bounded sample
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+Timing: each rotation pass (one launch per weight copy) is captured once into
+a HIP graph and replayed; HIP events on the kernels' own stream bracket every
+pass, the reported time per step is the median over passes.  Outputs are
+checked bit-for-bit against an untimed call before and after the timed region.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+    python bench.py --pmc-workload     # headline plan + a plain copy, for rocprofv3 --pmc
 """
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -27,6 +37,8 @@ HBM_PEAK_GBPS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 METRIC = "GEMV R1 µs & HBM GB/s (% peak); prefill GEMM TFLOP/s (% MFMA peak)"
 ROTATION_BYTES = 1 << 30
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+HEADLINE_KERNEL = "stx::gemv_kernel<4, 2, 1>"
 
 
 def log(msg):
@@ -34,47 +46,57 @@ def log(msg):
 
 
 class Rotation:
-    """Distinct device copies of one layer, each with its own prepared plan.
+    """Distinct device copies of one layer (or one group set), one prepared plan each.
 
-    One pass over the copies is captured into a HIP graph (one plan submission
-    per copy) so that the timed region measures the GPU, not Python's launch
-    rate.  The copies share x, y and the workspace (their calls are ordered on
-    one stream).
+    One pass over the copies is captured into a HIP graph so that the timed
+    region measures the GPU, not Python's launch rate.  The copies share x, y
+    and the workspace (their calls are ordered on one stream), so after any
+    number of passes y holds the result of one call.
     """
 
-    def __init__(self, ctx, I, N, K, R, seed, op="gemv", min_bytes=ROTATION_BYTES):
+    def __init__(self, ctx, I, N, K, R, seed, op="gemv", groups=1, min_bytes=ROTATION_BYTES):
         import torch
         import synth
         from strix_trellis import runtime
-        tr, suh, svh, _ = synth.layer(I, N, K, seed)
-        packed = I * N * K // 8
+        self.groups = groups
+        layers = [synth.layer(I, N, K, seed + g) for g in range(groups)]
+        packed = groups * I * N * K // 8
         self.copies = max(2, -(-min_bytes // packed))
         self.packed = packed
         self.stream = torch.cuda.Stream()
-        self.x = torch.from_numpy(synth.activations(R, I, seed + 1)).to("cuda:0")
-        self.y = torch.empty((R, N), device="cuda:0")
+        self.x = torch.from_numpy(synth.activations(R, groups * I, seed + 100)).to("cuda:0")
+        self.y = torch.empty((R, groups * N), device="cuda:0")
         self.weights, self.plans = [], []
         ws = None
         for _ in range(self.copies):
-            w = runtime.Weights(ctx, tr, suh, svh, None, "mul1")
-            if ws is None:
-                ws = runtime.alloc_workspace(runtime.workspace_bytes(w, self.x, self.y), "cuda:0")
-            self.weights.append(w)
-            self.plans.append(runtime.LinearPlan(w, self.x, self.y, workspace=ws, stream=self.stream, operation=op))
+            wl = [runtime.Weights(ctx, tr, suh, svh, None, "mul1") for (tr, suh, svh, _) in layers]
+            self.weights.extend(wl)
+            if op == "grouped":
+                # a grouped plan keeps its weight table in its own workspace
+                plan = runtime.GroupedGemvPlan(wl, self.x, self.y, R, igs=I, ogs=N, irs=groups * I,
+                                               ors=groups * N, stream=self.stream)
+            else:
+                if ws is None:
+                    ws = runtime.alloc_workspace(runtime.workspace_bytes(wl[0], self.x, self.y), "cuda:0")
+                plan = runtime.LinearPlan(wl[0], self.x, self.y, workspace=ws, stream=self.stream, operation=op)
+            self.plans.append(plan)
         self.workspace = ws
-        self.launches = self.plans[0].launches()
+        self.launches = self.plans[0].launches() if op != "grouped" else 1
         torch.cuda.synchronize()
+        self.plans[0].submit()
+        torch.cuda.synchronize()
+        self.expected = self.y.clone()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=self.stream):
             for p in self.plans:
                 p.submit()
         torch.cuda.synchronize()
 
-    def run(self, steps, start=0):
-        """Replay whole passes; `steps` is rounded up to a multiple of the copy count."""
-        for _ in range(-(-steps // self.copies)):
-            self.graph.replay()
-        return -(-steps // self.copies) * self.copies
+    def check(self):
+        """The replayed plans reproduce the untimed call bit for bit."""
+        import torch
+        torch.cuda.synchronize()
+        return bool(torch.equal(self.y.view(torch.int32), self.expected.view(torch.int32)))
 
     def close(self):
         del self.graph
@@ -84,47 +106,70 @@ class Rotation:
             w.destroy()
 
 
-def time_steps(run, steps, warmup, stream):
-    """HIP events on the stream the kernels run on; returns ms per step."""
+def time_rotation(rot, steps, warmup):
+    """Median over passes of (pass time / copies) in ms, HIP events on the plans' stream."""
     import torch
-    run(warmup)
+    passes = max(3, -(-steps // rot.copies))
+    for _ in range(max(1, -(-warmup // rot.copies))):
+        rot.graph.replay()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        done = run(steps)
-        end.record(stream)
+    ok_before = rot.check()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(passes + 1)]
+    with torch.cuda.stream(rot.stream):
+        ev[0].record(rot.stream)
+        for i in range(passes):
+            rot.graph.replay()
+            ev[i + 1].record(rot.stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / done, done
+    per_pass = [ev[i].elapsed_time(ev[i + 1]) / rot.copies for i in range(passes)]
+    ok_after = rot.check()
+    return {"ms": statistics.median(per_pass), "mean_ms": sum(per_pass) / passes,
+            "timed_steps": passes * rot.copies, "passes": passes, "output_check": ok_before and ok_after}
 
 
 def bench_gemv(ctx, I, N, K, R, steps, warmup, seed):
     rot = Rotation(ctx, I, N, K, R, seed, "gemv")
     try:
-        ms, steps = time_steps(rot.run, steps, warmup, rot.stream)
+        t = time_rotation(rot, steps, warmup)
     finally:
         rot.close()
-    us = ms * 1e3
-    gbps = rot.packed / (ms * 1e-3) / 1e9
-    return {"I": I, "N": N, "K": K, "R": R, "us": round(us, 3), "packed_GBps": round(gbps, 1),
+    gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
+    return {"I": I, "N": N, "K": K, "R": R, "us": round(t["ms"] * 1e3, 3), "packed_GBps": round(gbps, 1),
             "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "launches": rot.launches,
-            "rotation_copies": rot.copies, "timed_steps": steps}
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
 
 
 def bench_gemm(ctx, M, I, N, K, steps, warmup, seed):
-    rot = Rotation(ctx, I, N, K, M, seed, "gemm", min_bytes=ROTATION_BYTES // 4)
+    rot = Rotation(ctx, I, N, K, M, seed, "gemm")
     try:
-        ms, steps = time_steps(rot.run, steps, warmup, rot.stream)
+        t = time_rotation(rot, steps, warmup)
     finally:
         rot.close()
-    tflops = 2.0 * M * I * N / (ms * 1e-3) / 1e12
-    return {"M": M, "I": I, "N": N, "K": K, "us": round(ms * 1e3, 2), "TFLOPs": round(tflops, 1),
+    tflops = 2.0 * M * I * N / (t["ms"] * 1e-3) / 1e12
+    return {"M": M, "I": I, "N": N, "K": K, "us": round(t["ms"] * 1e3, 2), "TFLOPs": round(tflops, 1),
             "pct_fp16_peak": round(100 * tflops / FP16_PEAK_TFLOPS, 1), "launches": rot.launches,
-            "rotation_copies": rot.copies, "timed_steps": steps}
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
+
+
+def bench_grouped(ctx, G, I, N, K, R, steps, warmup, seed):
+    rot = Rotation(ctx, I, N, K, R, seed, "grouped", groups=G)
+    try:
+        t = time_rotation(rot, steps, warmup)
+    finally:
+        rot.close()
+    gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
+    return {"groups": G, "I": I, "N": N, "K": K, "R": R, "us": round(t["ms"] * 1e3, 3),
+            "packed_GBps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1),
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
 
 
 def cpu_baseline(sample_seconds=12.0):
-    """NumPy oracle (decode + staged FP32 layer) on the north-star layer, host cores."""
+    """NumPy oracle (decode + staged FP32 layer) on the north-star layer, host cores.
+
+    Phases timed separately: (i) vectorized decode of the packed layer, (ii)
+    the staged FP32 path from x to y given the decoded weights.  NumPy's
+    elementwise work runs on one thread.
+    """
     import numpy as np
     import synth
     from oracle import codec, linear
@@ -132,18 +177,25 @@ def cpu_baseline(sample_seconds=12.0):
     K = 4
     tr, suh, svh, _ = synth.layer(I, N, K, synth.BASE_SEED)
     x = synth.activations(1, I, synth.BASE_SEED + 1)
-    runs, t0 = 0, time.perf_counter()
+    dec, stg = [], []
+    t0 = time.perf_counter()
     while True:
+        a = time.perf_counter()
         q = codec.dequantize_rotated(tr, K)
+        b = time.perf_counter()
         linear.matmul_fp32_stages(x, tr, suh, svh, K, rotated=q)
-        runs += 1
-        if time.perf_counter() - t0 >= sample_seconds:
+        c = time.perf_counter()
+        dec.append(b - a)
+        stg.append(c - b)
+        if c - t0 >= sample_seconds and len(dec) >= 5:
             break
-    dt = (time.perf_counter() - t0) / runs
+    layer = statistics.median(d + s for d, s in zip(dec, stg))
     packed = I * N * K // 8
-    return {"value": round(packed / dt / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{runs} full R1 K4 4096x4096 layers (vectorized decode + staged FP32 path), "
-                      f"{dt * 1e3:.0f} ms each", "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
+    return {"value": round(packed / layer / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{len(dec)} full R1 K4 mul1 4096x4096 layers (vectorized decode + staged FP32 path), "
+                      f"median {layer * 1e3:.0f} ms per layer",
+            "decode_ms": round(statistics.median(dec) * 1e3, 1), "staged_ms": round(statistics.median(stg) * 1e3, 1),
+            "us_per_call": round(layer * 1e6, 1), "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
 
 
 def _cpu_model():
@@ -156,13 +208,43 @@ def _cpu_model():
     return "unknown"
 
 
+def _traffic():
+    """HBM bytes per headline launch from the committed rocprofv3 --pmc passes, if present."""
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+        return t.get(HEADLINE_KERNEL, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def pmc_workload(ctx, launches):
+    """Fixed workload for counter passes: the headline plan over its rotation,
+    launched directly (no graph), then a plain 256 MiB device copy whose
+    FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes."""
+    import torch
+    import synth
+    rot = Rotation(ctx, 4096, 4096, 4, 1, synth.BASE_SEED, "gemv")
+    for i in range(launches):
+        rot.plans[i % rot.copies].submit()
+    torch.cuda.synchronize()
+    ok = rot.check()
+    rot.close()
+    src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc workload: {launches} headline launches (bit_identical={ok}), 4 copies of {src.numel() * 4} bytes")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000)
-    ap.add_argument("--warmup", type=int, default=400)
-    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--steps", type=int, default=4096)
+    ap.add_argument("--warmup", type=int, default=512)
+    ap.add_argument("--quick", action="store_true", help="headline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-workload", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (every box here has one MI355X); --gpus {args.gpus} "
@@ -175,20 +257,35 @@ def main():
     ctx = runtime.Context(0)
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+    if args.pmc_workload:
+        pmc_workload(ctx, 256)
+        return
 
-    log("headline: R1 K4 4096x4096")
+    log("headline: GEMV R1 K4 4096x4096")
     head = bench_gemv(ctx, 4096, 4096, 4, 1, args.steps, args.warmup, synth.BASE_SEED)
     log(json.dumps(head))
-    sweep = []
-    if not args.no_sweep:
+    small_steps, small_warm = max(256, args.steps // 8), max(32, args.warmup // 8)
+    sweep, gemm, grouped = [], [], []
+    if not args.quick:
         for (I, N) in ((5120, 5120), (4096, 12288)):
             for K in (4, 5, 6):
                 for R in (1, 2, 4, 8):
-                    cell = bench_gemv(ctx, I, N, K, R, max(200, args.steps // 8), max(20, args.warmup // 8),
-                                      synth.BASE_SEED + 1)
+                    cell = bench_gemv(ctx, I, N, K, R, small_steps, small_warm, synth.BASE_SEED + 1)
                     log(json.dumps(cell))
                     sweep.append(cell)
+        for (I, N) in ((4096, 12288), (5120, 5120)):
+            for K in (4, 5, 6):
+                for M in (128, 512, 2048):
+                    cell = bench_gemm(ctx, M, I, N, K, 48, 8, synth.BASE_SEED + 2)
+                    log(json.dumps(cell))
+                    gemm.append(cell)
+        for R in range(1, 9):
+            cell = bench_grouped(ctx, 16, 4096, 1024, 5, R, small_steps, small_warm, synth.BASE_SEED + 3)
+            log(json.dumps(cell))
+            grouped.append(cell)
     cpu = None if args.no_cpu else cpu_baseline()
+    if cpu:
+        log(json.dumps(cpu))
     ms = head["us"] / 1e3
     achieved = head["packed_GBps"]
     out = {
@@ -202,18 +299,27 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 operands, f32 accumulation (K4 mul1 trellis)",
-        "data": "synthetic: PCG64 seed 20261201 trellis/suh/svh/x per BASELINE configs",
+        "dtype": "u16 trellis decode -> fp16 operands, f32 accumulation",
+        "data": f"synthetic: PCG64 seed {synth.BASE_SEED} (+ config index) trellis/suh/svh/x per BASELINE configs",
         "config": {"workload": "decode GEMV R1, EXL3 K4 mul1, I=N=4096, prepared single-launch plan, "
                                f"cold rotation over {head['rotation_copies']} weight copies (>=1 GiB)",
-                   "us_per_call": head["us"], "pct_hbm_peak": head["pct_hbm_peak"]},
+                   "us_per_call": head["us"], "pct_hbm_peak": head["pct_hbm_peak"],
+                   "bit_identical": head["bit_identical"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "stx::gemv_kernel<4,2,1>",
-                     "algorithmic_bytes_per_launch": 4096 * 4096 * 4 // 8},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _traffic(),
+                     "kernel": HEADLINE_KERNEL, "algorithmic_bytes_per_launch": 4096 * 4096 * 4 // 8,
+                     "launch_us": head["us"]},
         "cpu_baseline": cpu,
         "sweep_gemv": sweep,
+        "sweep_gemm": gemm,
+        "grouped_o_a": grouped,
     }
+    if gemm:
+        best = {}
+        for c in gemm:
+            if c["M"] == 2048:
+                best[f"{c['I']}x{c['N']} K{c['K']}"] = c["pct_fp16_peak"]
+        out["prefill_m2048_pct_fp16_peak"] = best
     print(json.dumps(out), flush=True)
 
 

@@ -13,10 +13,8 @@ Contents
 ``linear``  the FP64 algebraic layer and the staged FP32/RN16 production
             contract (restates python/strix_trellis/linear.py and
             docs/NUMERICS.md:30-126).
-``moe``     the routed-expert (SwiGLU + ordered weighted top-k) block on top of
-            ``linear`` (restates docs/TP_RANK.md:64-76 and
-            include/strix_trellis.h:197-233).
-``native``  ctypes loader for the C restatement in ``oracle/c`` (a faster
-            decode and a scalar FP32 core of the same contract), used where
-            the NumPy forms would be too slow for a test.
+``_ref``    (built, not committed) ``libstrix_ref.so``: the reference's own
+            scalar host oracle (src/host_reference.hpp) compiled from the
+            reference tree by ``make -C oracle ref``; tests use it to pin
+            ``codec`` state by state.
 """
