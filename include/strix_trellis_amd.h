@@ -41,6 +41,13 @@ strix_status strix_amd_gemv_shape(strix_weights weights, uint32_t *blocks_per_sp
  * single-launch GEMV plan). */
 strix_status strix_amd_plan_launches(strix_linear_plan plan, uint32_t *launches);
 
+/* Routed-expert activation on device F32 buffers: hidden[i] = SwiGLU(gate[i], up[i])
+ * with the arithmetic the MoE gate/up finish applies (stable sigmoid over the
+ * library's own exp; reference src/tp_moe_activation.hpp:46-60 for the form).
+ * Exposes that activation for bit-level checks; count 0 launches nothing. */
+strix_status strix_amd_swiglu(strix_context context, const float *gate, const float *up, float *hidden,
+    uint64_t count, const strix_stream *stream);
+
 #ifdef __cplusplus
 }
 #endif

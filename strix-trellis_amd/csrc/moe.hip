@@ -1,0 +1,58 @@
+// Host side of the routed-expert block: split policy, workspace sizes, launches.
+#include "moe_kernel.hpp"
+
+namespace stx {
+
+MoeSplit moe_split(uint32_t input) {
+    const uint32_t blocks = input / 16;
+    uint32_t bps = 8;
+    for (uint32_t b = 16; b <= uint32_t(MOE_MAX_BPS); b += 8)
+        if (blocks % b == 0) bps = b;
+    return {bps, blocks / bps};
+}
+
+uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H) {
+    return uint64_t(routes) * moe_split(I).splits * 2 * H + uint64_t(routes) * moe_split(H).splits * I;
+}
+
+uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H) {
+    return uint64_t(routes) * (H / 128) + uint64_t(rows) * (I / 128);
+}
+
+using MoeDispatch = hipError_t (*)(const MoeArgs&, hipStream_t);
+static const MoeDispatch gate_up_table[2] = {moe_gate_up_dispatch<2>, moe_gate_up_dispatch<3>};
+static const MoeDispatch down_table[2] = {moe_down_dispatch<2>, moe_down_dispatch<3>};
+
+static bool moe_args_ok(const MoeArgs& a) {
+    const uint32_t routes = a.rows * a.topk;
+    return a.rows >= 1 && a.rows <= 8 && a.topk >= 1 && a.topk <= MOE_MAX_TOPK && routes <= MOE_MAX_ROUTES &&
+           a.I % 128 == 0 && a.H % 128 == 0 && a.gate_bits >= 2 && a.gate_bits <= 3 && a.up_bits >= 2 &&
+           a.up_bits <= 3 && a.down_bits >= 2 && a.down_bits <= 3 && a.bps_gu <= uint32_t(MOE_MAX_BPS) &&
+           a.bps_d <= uint32_t(MOE_MAX_BPS) && a.bps_gu % 8 == 0 && a.bps_d % 8 == 0 &&
+           a.bps_gu * a.s_gu * 16 == a.I && a.bps_d * a.s_d * 16 == a.H;
+}
+
+hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t stream) {
+    if (!moe_args_ok(a)) return hipErrorInvalidValue;
+    return gate_up_table[a.gate_bits - 2](a, stream);
+}
+
+hipError_t launch_moe_down(const MoeArgs& a, hipStream_t stream) {
+    if (!moe_args_ok(a)) return hipErrorInvalidValue;
+    return down_table[a.down_bits - 2](a, stream);
+}
+
+__global__ __launch_bounds__(256) void moe_swiglu_kernel(const float* g, const float* u, float* h, uint64_t n) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) h[i] = moe_swiglu(g[i], u[i]);
+}
+
+hipError_t launch_moe_swiglu(const float* g, const float* u, float* h, uint64_t n, hipStream_t stream) {
+    if (!n) return hipSuccess;
+    const uint64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_swiglu_kernel, dim3(uint32_t(blocks)), dim3(256), 0, stream, g, u, h, n);
+    return hipGetLastError();
+}
+
+}  // namespace stx

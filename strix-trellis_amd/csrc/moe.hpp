@@ -1,0 +1,62 @@
+// Routed-expert (MoE) block: host-side launch interface.
+//
+// Operator (reference docs/TP_RANK.md:64-76, include/strix_trellis.h:207-233):
+//   hidden[r,s] = SwiGLU(gate_e(X[r]), up_e(X[r]))        e = ids[r,s]
+//   Y[r]        = alpha * sum_s(score[r,s] * down_e(hidden[r,s])) + beta * Y[r]
+// Every projection is a complete EXL3 linear (input stage, core, output
+// stage with svh and bias).  The slot sum runs s = 0..k-1 from +0, each term
+// RN32(score * value) added with one FP32 rounding; an exactly zero score
+// skips its term and reads neither hidden values nor down weights.  A token
+// whose routes are invalid (id outside the bank, repeated id, non-finite or
+// negative score) gets an all-NaN output row; no invalid id reaches the bank.
+//
+// Both launches take the routes as device buffers [rows][k] of bank indices;
+// the plans built from host routes upload them once.  The union of experts is
+// resolved inside the kernels: the first valid occurrence of an expert in
+// row-major route order leads its group, every other occurrence's workgroups
+// exit, so each expert's weights are streamed once for all its tokens.
+#pragma once
+#include "backend.hpp"
+
+namespace stx {
+
+struct MoeExpert {
+    GroupWeights gate, up, down;
+};
+
+constexpr uint32_t MOE_MAX_ROUTES = 64;   // rows * k: one wave resolves all of them
+constexpr uint32_t MOE_MAX_TOPK = 8;
+
+struct MoeArgs {
+    const MoeExpert* bank;
+    const uint32_t* ids;      // [rows][k] bank indices
+    const float* scores;      // [rows][k]
+    const float* x;           // [rows][x_stride], width I
+    float* y;                 // [rows][y_stride], width I
+    float* hidden;            // [rows][k][H] F32
+    float* p_gu;              // [rows*k][s_gu][2][H] partial planes of gate (0) and up (1)
+    float* p_d;               // [rows*k][s_d][I] partial planes of down
+    uint32_t* c_gu;           // [rows*k][H/128] arrival counters, zero between launches
+    uint32_t* c_d;            // [rows][I/128]
+    uint64_t x_stride, y_stride;
+    uint32_t bank_count, rows, topk, I, H;
+    uint32_t s_gu, bps_gu, s_d, bps_d;
+    uint32_t gate_bits, up_bits, down_bits;
+    float alpha, beta;
+};
+
+// Split-K decomposition of one MoE projection with `blocks` 16-channel input
+// blocks: the largest whole-H128 split of at most 32 blocks.
+struct MoeSplit {
+    uint32_t bps, splits;
+};
+MoeSplit moe_split(uint32_t input);
+uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
+uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H);
+
+hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t stream);
+hipError_t launch_moe_down(const MoeArgs& a, hipStream_t stream);
+// Diagnostic: h[i] = SwiGLU(g[i], u[i]) with the block's activation arithmetic.
+hipError_t launch_moe_swiglu(const float* g, const float* u, float* h, uint64_t n, hipStream_t stream);
+
+}  // namespace stx

@@ -1,0 +1,454 @@
+// Routed-expert (MoE) kernels for gfx950: grouped gate/up + SwiGLU, and down
+// with the ordered score-weighted top-k fold.
+//
+// Both launches reuse the GEMV building blocks (in-register trellis decode,
+// v_dot2 chains, LDS wave fold, coherent partial planes, last-arrival finish)
+// with routed rows instead of a fixed row range:
+//
+//   gate/up : grid (H/128, rows*k, s_gu), 256 threads.  Workgroup (c, j, s)
+//             belongs to route j; it works only if j leads its expert's group
+//             (first valid occurrence in route order).  It gathers the group's
+//             non-zero-score token rows of X, streams gate AND up tiles of
+//             column group c over input split s and writes both partial
+//             planes; the last split to arrive folds them, applies both output
+//             stages and SwiGLU and writes hidden[r, slot, 128c .. 128c+127].
+//   down    : grid (I/128, rows*k, s_d).  The group leader streams the down
+//             tiles once for all its rows (input = hidden of each row) and
+//             writes one plane per row; every workgroup of a group then
+//             arrives at the counter of each member token.  The last arrival
+//             for token r folds each slot's planes in ascending slot order,
+//             applies that slot's output stage, weights it by its score and
+//             finishes alpha/beta.  Invalid tokens get NaN rows.
+//
+// Accumulation order per projection (fixes the bits; independent of which
+// other tokens are routed to the same expert): lane chain over the wave's
+// blocks w, w+4, ... in ascending order; wave fold 0..3; split fold ascending
+// from +0 — the GEMV order of the same split decomposition.
+#pragma once
+#include "moe.hpp"
+#include "gemv_kernel.hpp"
+
+namespace stx {
+
+// ---------------------------------------------------------------------------
+// Activation.  exp(x) for x <= 0, which is all the stable sigmoid needs:
+// Cody–Waite reduction x = n*ln2 + r with |r| <= ln2/2, ln2 split into a head
+// with 16 significant bits (n*head is exact for |n| <= 256) and a tail; exp(r)
+// by its degree-7 Taylor polynomial in Horner form (truncation below 6e-9
+// relative); 2^n applied as two power-of-two factors so that a subnormal
+// result is rounded once.  Every step is a single FP32 operation, so a host
+// restatement with the same operations gives the same bits.
+// ---------------------------------------------------------------------------
+constexpr float MOE_LOG2E = 1.44269504088896341f;
+constexpr float MOE_LN2_HEAD = 0x1.62e4p-1f;             // 0.693145751953125
+constexpr float MOE_LN2_TAIL = 1.42860682030941723e-6f;  // RN32(ln2 - head)
+constexpr float MOE_INV_FACT[8] = {1.0f, 1.0f, 1.0f / 2, 1.0f / 6, 1.0f / 24, 1.0f / 120, 1.0f / 720, 1.0f / 5040};
+
+__device__ __forceinline__ float moe_pow2(int k) { return __builtin_bit_cast(float, uint32_t(k + 127) << 23); }
+
+__device__ __forceinline__ float moe_exp_nonpos(float x) {
+    if (!(x == x)) return x;
+    if (x < -104.0f) return 0.0f;
+    const float n = __builtin_rintf(x * MOE_LOG2E);
+    const float r = (x - n * MOE_LN2_HEAD) - n * MOE_LN2_TAIL;
+    float p = MOE_INV_FACT[7];
+#pragma unroll
+    for (int k = 6; k >= 0; --k) p = p * r + MOE_INV_FACT[k];
+    const int ni = int(n), n1 = ni / 2, n2 = ni - n1;
+    return (p * moe_pow2(n1)) * moe_pow2(n2);
+}
+
+// SwiGLU of one hidden element: g * sigmoid(g) * u, sigmoid in the stable
+// form 1/(1+e^-g) for g >= 0 and e^g/(1+e^g) for g < 0 (reference
+// src/tp_moe_activation.hpp:46-60), divisions correctly rounded.
+__device__ __forceinline__ float moe_swiglu(float g, float u) {
+    const bool neg = g < 0.0f;
+    const float ex = moe_exp_nonpos(neg ? g : -g);
+    const float den = 1.0f + ex;
+    const float sig = neg ? __fdiv_rn(ex, den) : __fdiv_rn(1.0f, den);
+    const float act = rn32(g * sig);
+    return rn32(act * u);
+}
+
+// ---------------------------------------------------------------------------
+// Route resolution (wave 0; one lane per route j = r*k + slot, rows*k <= 64).
+// ---------------------------------------------------------------------------
+struct MoeGroup {
+    uint64_t members;   // valid routes selecting this group's expert
+    uint64_t active;    // members with a non-zero score
+    uint32_t expert;
+    int leader;         // this workgroup's route leads the group
+    int token_valid;    // the route's token passes every check
+};
+
+__device__ __forceinline__ void moe_resolve(const MoeArgs& a, uint32_t route, MoeGroup* out) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t k = a.topk, n = a.rows * k;
+    const bool live = uint32_t(lane) < n;
+    const uint32_t id = ld_global(a.ids + (live ? lane : 0));
+    const float sc = ld_global(a.scores + (live ? lane : 0));
+    const uint32_t row = uint32_t(lane) / k, slot = uint32_t(lane) - row * k;
+    bool ok = live && id < a.bank_count && __builtin_isfinite(sc) && sc >= 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < MOE_MAX_TOPK; ++q) {
+        const uint32_t src = q < k ? row * k + q : uint32_t(lane);
+        const uint32_t other = __shfl(id, int(src & 63), 64);
+        if (q < k && q != slot && other == id) ok = false;
+    }
+    const uint64_t bad = __ballot(live && !ok);
+    const uint64_t row_bits = live ? ((1ull << k) - 1) << (row * k) : 0;   // k <= 8, row*k + k <= 64
+    const bool tv = live && (bad & row_bits) == 0;
+    const uint32_t e = __shfl(id, int(route), 64);
+    const int tv_route = __shfl(int(tv), int(route), 64);
+    const uint64_t members = __ballot(tv && id == e);
+    const uint64_t active = members & __ballot(sc != 0.0f);
+    if (lane == 0) {
+        out->members = members;
+        out->active = active;
+        out->expert = e;
+        out->token_valid = tv_route;
+        out->leader = tv_route && (members & ((1ull << route) - 1)) == 0;
+    }
+}
+
+// Route index of the i-th set bit of m (i < popcount(m)).
+__device__ __forceinline__ uint32_t moe_nth_route(uint64_t m, int i) {
+    for (int q = 0; q < i; ++q) m &= m - 1;
+    return uint32_t(__builtin_ctzll(m));
+}
+
+// Fold `splits` planes (stride between splits `step` floats) at p, p+64.
+__device__ __forceinline__ void moe_fold(const float* p, uint32_t splits, uint64_t step, float& z0, float& z1) {
+    const int lane = threadIdx.x & 63;
+    z0 = 0.0f;
+    z1 = 0.0f;
+    uint32_t s = 0;
+    for (; s + 8 <= splits; s += 8) {
+        float v0[8], v1[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            v0[u] = load_coherent(p + (s + u) * step + lane);
+            v1[u] = load_coherent(p + (s + u) * step + lane + 64);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            z0 = z0 + v0[u];
+            z1 = z1 + v1[u];
+        }
+    }
+    for (; s < splits; ++s) {
+        z0 = z0 + load_coherent(p + s * step + lane);
+        z1 = z1 + load_coherent(p + s * step + lane + 64);
+    }
+}
+
+// Every store of this workgroup is complete before any of its threads goes on
+// to arrive at a counter.
+__device__ __forceinline__ void moe_release() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+}
+
+constexpr int MOE_MAX_BPS = 32;
+constexpr int MOE_MAX_RT = 8;
+
+// ---------------------------------------------------------------------------
+// Gate/up core of one workgroup: NP = 2 projections sharing the routed rows.
+// ---------------------------------------------------------------------------
+template <int KG, int KU, int RT>
+__device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpert& ex, uint32_t c, uint32_t split,
+                                                 uint64_t active, int nrows, _Float16* act, float* red) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int jt = lane >> 3, g = lane & 7;
+    const uint32_t bps = a.bps_gu, a0 = split * bps;
+    const uint32_t act_row = bps * 16;
+    constexpr uint32_t tg = 32u * KG, tu = 32u * KU;
+    const uint32_t rbg = (a.H >> 4) * tg, rbu = (a.H >> 4) * tu;
+    const auto rg = make_rsrc(reinterpret_cast<const char*>(ex.gate.trellis) + uint64_t(a0) * rbg, bps * rbg);
+    const auto ru = make_rsrc(reinterpret_cast<const char*>(ex.up.trellis) + uint64_t(a0) * rbu, bps * rbu);
+    const uint32_t og = (8u * c + jt) * tg + g * 4u * KG, ou = (8u * c + jt) * tu + g * 4u * KU;
+    const int nb = int(bps) / GEMV_WAVES;
+    constexpr uint32_t kOut = 0x80000000u;
+    auto offg = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbg + og : kOut; };
+    auto offu = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbu + ou : kOut; };
+
+    Chunk<KG> cg[2];
+    Chunk<KU> cu[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        load_chunk(cg[u], rg, offg(u));
+        load_chunk(cu[u], ru, offu(u));
+    }
+
+    // Input stages (gate and up have their own suh): one 128-block per wave and unit.
+    const int hblocks = int(bps) / 8, per_proj = nrows * hblocks;
+    for (int u = w; u < 2 * per_proj; u += GEMV_WAVES) {
+        const int p = u / per_proj, v = u - p * per_proj;
+        const int i = v / hblocks, hb = v - i * hblocks;
+        const uint32_t r = moe_nth_route(active, i) / a.topk;
+        const uint32_t ch = a0 * 16 + hb * 128;
+        const uint16_t* suh = p ? ex.up.suh : ex.gate.suh;
+        input_block(a.x + r * a.x_stride + ch, suh + ch, act + (p * MOE_MAX_RT + i) * act_row + hb * 128, true);
+    }
+    // Rows past nrows stay unused: dot_block reads only rows < RT and the
+    // fold below only rows < nrows; rows nrows..RT-1 hold stale LDS and their
+    // sums are discarded.
+    __syncthreads();
+
+    float accg[RT][2], accu[RT][2];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) accg[r][0] = accg[r][1] = accu[r][0] = accu[r][1] = 0.0f;
+    const bool first = g == 0;
+    for (int t = 0; t < nb; t += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (t + u < nb) {
+                const int blk = w + GEMV_WAVES * (t + u);
+                half2_t wq[4][4];
+                link_chunk(cg[u], first);
+                decode_chunk<KG, CB_MUL1>(cg[u], wq);
+                dot_block<RT>(wq, act + blk * 16, act_row, accg);
+                link_chunk(cu[u], first);
+                decode_chunk<KU, CB_MUL1>(cu[u], wq);
+                dot_block<RT>(wq, act + MOE_MAX_RT * act_row + blk * 16, act_row, accu);
+            }
+            load_chunk(cg[u], rg, offg(t + u + 2));
+            load_chunk(cu[u], ru, offu(t + u + 2));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        red[((w * 2 + 0) * MOE_MAX_RT + r) * 128 + 16 * jt + g] = accg[r][0];
+        red[((w * 2 + 0) * MOE_MAX_RT + r) * 128 + 16 * jt + g + 8] = accg[r][1];
+        red[((w * 2 + 1) * MOE_MAX_RT + r) * 128 + 16 * jt + g] = accu[r][0];
+        red[((w * 2 + 1) * MOE_MAX_RT + r) * 128 + 16 * jt + g + 8] = accu[r][1];
+    }
+    __syncthreads();
+}
+
+template <int KG, int KU>
+__global__ __launch_bounds__(GEMV_THREADS) void moe_gate_up_kernel(MoeArgs a) {
+    __shared__ __align__(16) _Float16 act[2 * MOE_MAX_RT * MOE_MAX_BPS * 16];
+    __shared__ __align__(16) float red[GEMV_WAVES * 2 * MOE_MAX_RT * 128];
+    __shared__ MoeGroup grp;
+    __shared__ int last;
+    const uint32_t c = blockIdx.x, route = blockIdx.y, split = blockIdx.z;
+    const int tid = threadIdx.x, w = tid >> 6;
+    if (w == 0) moe_resolve(a, route, &grp);
+    __syncthreads();
+    if (!grp.leader || !grp.active) return;
+    const uint64_t active = grp.active;
+    const int nrows = __builtin_popcountll(active);
+    const MoeExpert& ex = a.bank[grp.expert];
+    if (nrows <= 1) moe_gate_up_core<KG, KU, 1>(a, ex, c, split, active, nrows, act, red);
+    else if (nrows <= 2) moe_gate_up_core<KG, KU, 2>(a, ex, c, split, active, nrows, act, red);
+    else if (nrows <= 4) moe_gate_up_core<KG, KU, 4>(a, ex, c, split, active, nrows, act, red);
+    else moe_gate_up_core<KG, KU, 8>(a, ex, c, split, active, nrows, act, red);
+
+    // Wave fold in wave order -> planes [route][split][proj][H].
+    const uint32_t S = a.s_gu, H = a.H;
+    for (int idx = tid; idx < 2 * nrows * 128; idx += GEMV_THREADS) {
+        const int n = idx & 127, pr = idx >> 7, p = pr & 1, i = pr >> 1;
+        float v = red[((0 * 2 + p) * MOE_MAX_RT + i) * 128 + n];
+#pragma unroll
+        for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + red[((ww * 2 + p) * MOE_MAX_RT + i) * 128 + n];
+        const uint32_t j = moe_nth_route(active, i);
+        store_coherent(a.p_gu + ((uint64_t(j) * S + split) * 2 + p) * H + 128 * c + n, v);
+    }
+    moe_release();
+    uint32_t* counter = a.c_gu + uint64_t(route) * (H >> 7) + c;
+    if (tid == 0) last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    __syncthreads();
+    if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+    // Last split: both output stages, SwiGLU, hidden.
+    const int lane = tid & 63;
+    const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
+    for (int i = w; i < nrows; i += GEMV_WAVES) {
+        const uint32_t j = moe_nth_route(active, i);
+        float g0, g1, u0, u1;
+        moe_fold(a.p_gu + (uint64_t(j) * S * 2 + 0) * H + 128 * c, S, 2ull * H, g0, g1);
+        moe_fold(a.p_gu + (uint64_t(j) * S * 2 + 1) * H + 128 * c, S, 2ull * H, u0, u1);
+        h32_wave(g0, g1);
+        h32_wave(u0, u1);
+        g0 = output_element(g0, ld_global(ex.gate.svh + n0), ex.gate.bias, n0, 1.0f, 0.0f, nullptr);
+        g1 = output_element(g1, ld_global(ex.gate.svh + n1), ex.gate.bias, n1, 1.0f, 0.0f, nullptr);
+        u0 = output_element(u0, ld_global(ex.up.svh + n0), ex.up.bias, n0, 1.0f, 0.0f, nullptr);
+        u1 = output_element(u1, ld_global(ex.up.svh + n1), ex.up.bias, n1, 1.0f, 0.0f, nullptr);
+        float* hrow = a.hidden + uint64_t(j) * H;
+        *(__attribute__((address_space(1))) float*)(hrow + n0) = moe_swiglu(g0, u0);
+        *(__attribute__((address_space(1))) float*)(hrow + n1) = moe_swiglu(g1, u1);
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Down core of one workgroup (one projection, rows = the group's active routes).
+// ---------------------------------------------------------------------------
+template <int K, int RT>
+__device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert& ex, uint32_t c, uint32_t split,
+                                              uint64_t active, int nrows, _Float16* act, float* red) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int jt = lane >> 3, g = lane & 7;
+    const uint32_t bps = a.bps_d, a0 = split * bps;
+    const uint32_t act_row = bps * 16;
+    constexpr uint32_t tb = 32u * K;
+    const uint32_t rb = (a.I >> 4) * tb;
+    const auto rs = make_rsrc(reinterpret_cast<const char*>(ex.down.trellis) + uint64_t(a0) * rb, bps * rb);
+    const uint32_t lo = (8u * c + jt) * tb + g * 4u * K;
+    const int nb = int(bps) / GEMV_WAVES;
+    constexpr uint32_t kOut = 0x80000000u;
+    auto off = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rb + lo : kOut; };
+
+    Chunk<K> ring[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_chunk(ring[u], rs, off(u));
+
+    const int hblocks = int(bps) / 8, units = nrows * hblocks;
+    for (int u = w; u < units; u += GEMV_WAVES) {
+        const int i = u / hblocks, hb = u - i * hblocks;
+        const uint32_t j = moe_nth_route(active, i);
+        const uint32_t ch = a0 * 16 + hb * 128;
+        input_block(a.hidden + uint64_t(j) * a.H + ch, ex.down.suh + ch, act + i * act_row + hb * 128, true);
+    }
+    __syncthreads();
+
+    float acc[RT][2];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+    const bool first = g == 0;
+    for (int t = 0; t < nb; t += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (t + u < nb) {
+                half2_t wq[4][4];
+                link_chunk(ring[u], first);
+                decode_chunk<K, CB_MUL1>(ring[u], wq);
+                dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+            }
+            load_chunk(ring[u], rs, off(t + u + 4));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        red[(w * MOE_MAX_RT + r) * 128 + 16 * jt + g] = acc[r][0];
+        red[(w * MOE_MAX_RT + r) * 128 + 16 * jt + g + 8] = acc[r][1];
+    }
+    __syncthreads();
+}
+
+template <int K>
+__global__ __launch_bounds__(GEMV_THREADS) void moe_down_kernel(MoeArgs a) {
+    __shared__ __align__(16) _Float16 act[MOE_MAX_RT * MOE_MAX_BPS * 16];
+    __shared__ __align__(16) float red[GEMV_WAVES * MOE_MAX_RT * 128];
+    __shared__ MoeGroup grp;
+    __shared__ uint32_t finish_mask;
+    const uint32_t c = blockIdx.x, route = blockIdx.y, split = blockIdx.z;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const uint32_t k = a.topk, I = a.I, S = a.s_d;
+    if (w == 0) moe_resolve(a, route, &grp);
+    __syncthreads();
+    if (!grp.token_valid) {
+        // One workgroup per (token, column group) writes the NaN row block.
+        if (route % k == 0 && split == 0 && tid < 128)
+            a.y[uint64_t(route / k) * a.y_stride + 128 * c + tid] = __builtin_bit_cast(float, 0x7fc00000u);
+        return;
+    }
+    if (!grp.leader) return;
+    const uint64_t active = grp.active, members = grp.members;
+    const int nrows = __builtin_popcountll(active);
+    const MoeExpert& ex = a.bank[grp.expert];
+    if (nrows) {
+        if (nrows <= 1) moe_down_core<K, 1>(a, ex, c, split, active, nrows, act, red);
+        else if (nrows <= 2) moe_down_core<K, 2>(a, ex, c, split, active, nrows, act, red);
+        else if (nrows <= 4) moe_down_core<K, 4>(a, ex, c, split, active, nrows, act, red);
+        else moe_down_core<K, 8>(a, ex, c, split, active, nrows, act, red);
+        for (int idx = tid; idx < nrows * 128; idx += GEMV_THREADS) {
+            const int n = idx & 127, i = idx >> 7;
+            float v = red[(0 * MOE_MAX_RT + i) * 128 + n];
+#pragma unroll
+            for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + red[(ww * MOE_MAX_RT + i) * 128 + n];
+            const uint32_t j = moe_nth_route(active, i);
+            store_coherent(a.p_d + (uint64_t(j) * S + split) * I + 128 * c + n, v);
+        }
+    }
+    moe_release();
+    // One arrival per member route (one route per token), lanes in parallel.
+    const uint32_t expected = k * S;
+    if (w == 0) {
+        const int nm = __builtin_popcountll(members);
+        bool fin = false;
+        uint32_t r = 0;
+        if (lane < nm) {
+            r = moe_nth_route(members, lane) / k;
+            uint32_t* counter = a.c_d + uint64_t(r) * (I >> 7) + c;
+            fin = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
+        }
+        const uint64_t fins = __ballot(fin);
+        uint32_t mask = 0;
+        for (uint64_t m = fins; m; m &= m - 1) mask |= 1u << __shfl(int(r), __builtin_ctzll(m), 64);
+        if (lane == 0) finish_mask = mask;
+    }
+    __syncthreads();
+    const uint32_t fm = finish_mask;
+    if (!fm) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+    // Tokens whose last arrival this was: ordered slot fold, alpha/beta.
+    const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
+    int q = 0;
+    for (uint32_t m = fm; m; m &= m - 1, ++q) {
+        if (q % GEMV_WAVES != w) continue;
+        const uint32_t r = uint32_t(__builtin_ctz(m));
+        float comb0 = 0.0f, comb1 = 0.0f;
+        for (uint32_t s = 0; s < k; ++s) {
+            const uint32_t j = r * k + s;
+            const float score = ld_global(a.scores + j);
+            if (score == 0.0f) continue;
+            const MoeExpert& es = a.bank[ld_global(a.ids + j)];
+            float z0, z1;
+            moe_fold(a.p_d + uint64_t(j) * S * I + 128 * c, S, I, z0, z1);
+            h32_wave(z0, z1);
+            z0 = output_element(z0, ld_global(es.down.svh + n0), es.down.bias, n0, 1.0f, 0.0f, nullptr);
+            z1 = output_element(z1, ld_global(es.down.svh + n1), es.down.bias, n1, 1.0f, 0.0f, nullptr);
+            comb0 = rn32(comb0 + rn32(score * z0));
+            comb1 = rn32(comb1 + rn32(score * z1));
+        }
+        float* yr = a.y + uint64_t(r) * a.y_stride;
+        float o0 = rn32(a.alpha * comb0), o1 = rn32(a.alpha * comb1);
+        if (a.beta != 0.0f) {
+            o0 = rn32(o0 + rn32(a.beta * ld_global(yr + n0)));
+            o1 = rn32(o1 + rn32(a.beta * ld_global(yr + n1)));
+        }
+        *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+        *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+        if (lane == 0) __hip_atomic_store(a.c_d + uint64_t(r) * (I >> 7) + c, 0u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+#define STX_INSTANTIATE_MOE(KG)                                                                                   \
+    template <>                                                                                                   \
+    hipError_t moe_gate_up_dispatch<KG>(const MoeArgs& a, hipStream_t s) {                                        \
+        const dim3 grid(a.H / 128, a.rows * a.topk, a.s_gu);                                                      \
+        if (a.up_bits == 2)                                                                                       \
+            hipLaunchKernelGGL((moe_gate_up_kernel<KG, 2>), grid, dim3(GEMV_THREADS), 0, s, a);                     \
+        else                                                                                                      \
+            hipLaunchKernelGGL((moe_gate_up_kernel<KG, 3>), grid, dim3(GEMV_THREADS), 0, s, a);                     \
+        return hipGetLastError();                                                                                 \
+    }                                                                                                             \
+    template <>                                                                                                   \
+    hipError_t moe_down_dispatch<KG>(const MoeArgs& a, hipStream_t s) {                                           \
+        hipLaunchKernelGGL(moe_down_kernel<KG>, dim3(a.I / 128, a.rows * a.topk, a.s_d), dim3(GEMV_THREADS), 0, s, \
+                           a);                                                                                    \
+        return hipGetLastError();                                                                                 \
+    }
+
+template <int KG>
+hipError_t moe_gate_up_dispatch(const MoeArgs& a, hipStream_t s);
+template <int K>
+hipError_t moe_down_dispatch(const MoeArgs& a, hipStream_t s);
+
+}  // namespace stx

@@ -164,6 +164,7 @@ _PROTOTYPES = {
     "strix_amd_output_stage": (_S, [vp, vp, u64, vp, u64, f32, f32, C.POINTER(Stream)]),
     "strix_amd_gemv_shape": (_S, [vp, C.POINTER(u32), C.POINTER(u32)]),
     "strix_amd_plan_launches": (_S, [vp, C.POINTER(u32)]),
+    "strix_amd_swiglu": (_S, [vp, vp, vp, vp, u64, C.POINTER(Stream)]),
 }
 
 _lib = None

@@ -266,3 +266,100 @@ class GroupedGemvPlan:
         if self.handle:
             abi.check(self.lib.strix_grouped_gemv_plan_destroy(self.handle), "strix_grouped_gemv_plan_destroy")
             self.handle = None
+
+
+def row_view_desc(t):
+    """F32 descriptor of a rank-2 row view (unit channel stride, any row stride)."""
+    if t.dtype != _t().float32 or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError("row views must be float32 [rows, width] with unit channel stride")
+    d = abi.header(abi.TensorDesc)
+    d.dtype = abi.DTYPE_F32
+    d.data = C.c_void_p(t.data_ptr() or None)
+    d.rank = 2
+    d.shape[0], d.shape[1] = t.shape[0], t.shape[1]
+    d.strides[0], d.strides[1] = t.stride(0), 1
+    d.buffer_bytes = ((t.shape[0] - 1) * t.stride(0) + t.shape[1]) * 4
+    return d
+
+
+class MoePlan:
+    """Routed-expert block y = alpha * sum_s score * down(SwiGLU(gate(x), up(x))) + beta * y.
+
+    ``experts`` is a list of (gate, up, down) Weights.  Host routes
+    (``ids``/``scores`` NumPy [rows, k]) name experts by ``expert_ids`` (default
+    0..E-1) and must use exactly the given experts; device routes
+    (``device_ids``/``device_scores`` torch int32/float32 [rows, k]) index the
+    bank, may be rewritten between submissions and are read by every launch.
+    """
+
+    def __init__(self, ctx, experts, x, y, ids=None, scores=None, expert_ids=None, device_ids=None,
+                 device_scores=None, alpha=1.0, beta=0.0, workspace=None, stream=None, split=False):
+        self.lib = ctx.lib
+        torch = _t()
+        n = len(experts)
+        arr = (abi.TpExpertDesc * n)()
+        for i, (g, u, dn) in enumerate(experts):
+            arr[i] = abi.header(abi.TpExpertDesc, expert_id=i if expert_ids is None else int(expert_ids[i]),
+                                gate=g.handle.value, up=u.handle.value, down=dn.handle.value)
+        self.stream = stream
+        sd = stream_desc(stream)
+        keep = [arr, experts, x, y]
+        rows = x.shape[0]
+        if device_ids is None:
+            ids_np = np.ascontiguousarray(ids, dtype=np.uint32)
+            sc_np = np.ascontiguousarray(scores, dtype=np.float32)
+            keep += [ids_np, sc_np]
+            d = abi.header(abi.TpMoeDesc, input=row_view_desc(x), output=row_view_desc(y),
+                           experts=C.cast(arr, C.POINTER(abi.TpExpertDesc)), expert_count=n,
+                           route_ids=ids_np.ctypes.data_as(C.POINTER(C.c_uint32)), route_ids_count=ids_np.size,
+                           route_scores=sc_np.ctypes.data_as(C.POINTER(C.c_float)),
+                           route_scores_count=sc_np.size, alpha=alpha, beta=beta)
+            k = ids_np.size // rows
+        else:
+            keep += [device_ids, device_scores]
+            d = abi.header(abi.TpMoeDeviceDesc, input=row_view_desc(x), output=row_view_desc(y),
+                           experts=C.cast(arr, C.POINTER(abi.TpExpertDesc)), expert_count=n,
+                           route_ids=C.c_void_p(device_ids.data_ptr()), route_ids_bytes=device_ids.numel() * 4,
+                           route_scores=C.c_void_p(device_scores.data_ptr()),
+                           route_scores_bytes=device_scores.numel() * 4, alpha=alpha, beta=beta)
+            k = device_ids.numel() // rows
+        H = experts[0][0].output
+        if workspace is None:
+            workspace = torch.empty(rows * k * H, dtype=torch.float32, device=x.device)
+        d.workspace = C.c_void_p(workspace.data_ptr())
+        d.workspace_bytes = workspace.numel() * workspace.element_size()
+        keep.append(workspace)
+        self.workspace = workspace
+        self.hidden = workspace[:rows * k * H].view(rows, k, H)
+        self._keep = keep
+        h = C.c_void_p()
+        if device_ids is None:
+            fn = self.lib.strix_tp_moe_plan_create_split if split else self.lib.strix_tp_moe_plan_create
+        else:
+            fn = self.lib.strix_tp_moe_plan_create_device_split if split else self.lib.strix_tp_moe_plan_create_device
+        abi.check(fn(ctx.handle, C.byref(d), C.byref(sd), C.byref(h)), fn.__name__)
+        self.handle = h
+
+    def submit(self):
+        abi.check(self.lib.strix_tp_moe_plan_submit(self.handle), "strix_tp_moe_plan_submit")
+
+    def gate_up(self):
+        abi.check(self.lib.strix_tp_moe_plan_gate_up(self.handle), "strix_tp_moe_plan_gate_up")
+
+    def down(self):
+        abi.check(self.lib.strix_tp_moe_plan_down(self.handle), "strix_tp_moe_plan_down")
+
+    def destroy(self):
+        if self.handle:
+            abi.check(self.lib.strix_tp_moe_plan_destroy(self.handle), "strix_tp_moe_plan_destroy")
+            self.handle = None
+
+
+def swiglu(ctx, gate, up, stream=None):
+    """Device SwiGLU of the routed-expert block on float32 tensors (diagnostic)."""
+    torch = _t()
+    h = torch.empty_like(gate)
+    abi.check(ctx.lib.strix_amd_swiglu(ctx.handle, C.c_void_p(gate.data_ptr()), C.c_void_p(up.data_ptr()),
+                                       C.c_void_p(h.data_ptr()), gate.numel(), C.byref(stream_desc(stream))),
+              "strix_amd_swiglu")
+    return h

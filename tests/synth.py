@@ -40,3 +40,28 @@ def gate(actual, reference):
     assert maxabs <= limit, f"maxabs {maxabs:.3e} > {limit:.3e}"
     assert nrmse <= 3e-5, f"nrmse {nrmse:.3e} > 3e-5"
     return maxabs, nrmse
+
+
+def moe_bank(E, I, H, K, seed, bias=False, bits=None):
+    """E experts, each dict(gate=(trellis, suh, svh, bias, K), up=..., down=...):
+    gate/up [I -> H], down [H -> I].  ``bits`` = (Kgate, Kup, Kdown) overrides K."""
+    kg, ku, kd = bits or (K, K, K)
+    bank = []
+    for e in range(E):
+        s = seed + 3 * e
+        g = layer(I, H, kg, s, bias)
+        u = layer(I, H, ku, s + 1, bias)
+        d = layer(H, I, kd, s + 2, bias)
+        bank.append({"gate": (*g, kg), "up": (*u, ku), "down": (*d, kd)})
+    return bank
+
+
+def routes(R, E, k, seed):
+    """Per token k distinct experts drawn uniformly (choice without replacement),
+    scores = float32 softmax of N(0,1) logits over the k selected."""
+    g = rng(seed)
+    ids = np.stack([g.choice(E, k, replace=False) for _ in range(R)]).astype(np.uint32)
+    logits = g.standard_normal((R, k))
+    sc = np.exp(logits - logits.max(axis=1, keepdims=True))
+    sc = (sc / sc.sum(axis=1, keepdims=True)).astype(np.float32)
+    return ids, sc

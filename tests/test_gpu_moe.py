@@ -1,0 +1,236 @@
+"""GPU parity of the routed-expert block (strix_tp_moe_* plans) through the C ABI.
+
+Bars:
+* the activation is bit-exact to the oracle's SwiGLU (its own exp);
+* hidden and the block output meet the reference GPU gate against the staged
+  FP32 oracle (the projections' cores accumulate in the GPU order);
+* identities that fix the bits exactly: host-route plan == device-route plan,
+  a token's output does not depend on the other tokens or on the order of the
+  expert array, a zero score removes its slot, invalid tokens give NaN rows
+  and leave the others untouched, alpha/beta apply on top of the same sum,
+  replays of a captured graph follow routes rewritten in place.
+"""
+import numpy as np
+import pytest
+
+import synth
+from oracle import moe
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from strix_trellis import abi, runtime  # noqa: E402
+
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    c = runtime.Context(0)
+    yield c
+    torch.cuda.synchronize()
+
+
+def _weights(ctx, bank):
+    out = []
+    for e in bank:
+        ws = []
+        for p in ("gate", "up", "down"):
+            tr, suh, svh, b, _ = e[p]
+            ws.append(runtime.Weights(ctx, tr, suh, svh, b, "mul1"))
+        out.append(tuple(ws))
+    return out
+
+
+def _destroy(ws):
+    for t in ws:
+        for w in t:
+            w.destroy()
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _run(ctx, ws, x, ids, sc, alpha=1.0, beta=0.0, old=None, device=False, expert_ids=None):
+    y = _dev(old) if old is not None else torch.full((x.shape[0], x.shape[1]), float("nan"), device=DEV)
+    xd = _dev(x)
+    if device:
+        di = _dev(ids.astype(np.int32))
+        ds = _dev(sc.astype(np.float32))
+        plan = runtime.MoePlan(ctx, ws, xd, y, device_ids=di, device_scores=ds, alpha=alpha, beta=beta)
+    else:
+        plan = runtime.MoePlan(ctx, ws, xd, y, ids=ids, scores=sc, expert_ids=expert_ids, alpha=alpha, beta=beta)
+    plan.submit()
+    torch.cuda.synchronize()
+    out, hidden = y.cpu().numpy(), plan.hidden.cpu().numpy()
+    plan.destroy()
+    return out, hidden
+
+
+def test_swiglu_bit_exact(ctx):
+    g = synth.rng(21).standard_normal(1 << 18).astype(np.float32) * np.float32(8)
+    u = synth.rng(22).standard_normal(1 << 18).astype(np.float32)
+    special = np.array([0.0, -0.0, 1e-40, -1e-40, 88.0, -88.0, 103.0, -103.0, 104.5, -104.5, 200.0, -200.0,
+                        np.inf, -np.inf, np.nan, 1.0, -1.0, 3.4e38, -3.4e38], np.float32)
+    g[:special.size] = special
+    u[:special.size] = 1.5
+    h = runtime.swiglu(ctx, _dev(g), _dev(u)).cpu().numpy()
+    ref = moe.swiglu(g, u)
+    same = (h.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(h) & np.isnan(ref))
+    assert same.all(), f"{np.count_nonzero(~same)} differ, first at {np.flatnonzero(~same)[:4]}"
+
+
+MOE_CASES = [
+    # (E, I, H, R, k, bits (gate, up, down), bias)
+    (6, 256, 128, 3, 2, (2, 2, 2), True),
+    (8, 512, 256, 4, 3, (3, 2, 3), False),
+    (5, 256, 384, 2, 4, (2, 3, 2), True),
+    (12, 1024, 256, 8, 6, (2, 2, 3), False),
+]
+
+
+@pytest.mark.parametrize("E,I,H,R,k,bits,bias", MOE_CASES)
+def test_block_matches_oracle(ctx, E, I, H, R, k, bits, bias):
+    print(f"moe E={E} I={I} H={H} R={R} k={k} bits={bits} bias={bias}", flush=True)
+    seed = 9000 + E + R
+    bank = synth.moe_bank(E, I, H, 2, seed, bias=bias, bits=bits)
+    ids, sc = synth.routes(R, E, k, seed + 50)
+    used = sorted(set(ids.ravel().tolist()))
+    # host plans take the exact union: relabel to the used experts
+    sub = [bank[e] for e in used]
+    remap = {e: i for i, e in enumerate(used)}
+    ids_u = np.vectorize(remap.get)(ids).astype(np.uint32)
+    x = synth.activations(R, I, seed + 60)
+    ws = _weights(ctx, sub)
+    y, hidden = _run(ctx, ws, x, ids_u, sc)
+    cache = {}
+    ref, href = moe.moe_block(x, sub, ids_u, sc, cache=cache)
+    # hidden = SwiGLU of two projections: twice the single-linear nrmse bar
+    a, r = hidden.reshape(-1, H).astype(np.float64), href.reshape(-1, H).astype(np.float64)
+    assert np.isfinite(a).all()
+    nrmse = np.sqrt(np.sum((a - r) ** 2) / np.sum(r ** 2))
+    assert np.max(np.abs(a - r)) <= 5e-4 * max(1.0, np.max(np.abs(r))) and nrmse <= 6e-5, nrmse
+    # the down half from the GPU's own hidden: the single-linear gate
+    synth.gate(y, moe.down_combine(hidden, sub, ids_u, sc, cache=cache))
+    # the whole chain (three projections) against the oracle: max-rel-err 1e-3
+    assert np.max(np.abs(y - ref)) <= 1e-3 * np.max(np.abs(ref))
+    # the same routes through a device bank of all E experts give the same bits
+    wall = _weights(ctx, bank)
+    yd, _ = _run(ctx, wall, x, ids, sc, device=True)
+    assert np.array_equal(yd.view(np.uint32), y.view(np.uint32))
+    _destroy(ws)
+    _destroy(wall)
+
+
+def test_block_identities(ctx):
+    E, I, H, R, k = 10, 512, 256, 6, 3
+    bank = synth.moe_bank(E, I, H, 2, 777, bias=True)
+    ids, sc = synth.routes(R, E, k, 778)
+    x = synth.activations(R, I, 779)
+    ws = _weights(ctx, bank)
+    y, _ = _run(ctx, ws, x, ids, sc, device=True)
+    # token independence: each token alone gives its own bits
+    for r in (0, 3, 5):
+        yr, _ = _run(ctx, ws, x[r:r + 1], ids[r:r + 1], sc[r:r + 1], device=True)
+        assert np.array_equal(yr.view(np.uint32), y[r:r + 1].view(np.uint32)), r
+    # the host plan with the expert array permuted (ids name experts by expert_id)
+    used = sorted(set(ids.ravel().tolist()))
+    order = used[::-1]
+    wsub = [ws[e] for e in order]
+    yh, _ = _run(ctx, wsub, x, ids, sc, expert_ids=order)
+    assert np.array_equal(yh.view(np.uint32), y.view(np.uint32))
+    # zero score: the slot disappears, other tokens unchanged
+    sc0 = sc.copy()
+    sc0[2, 1] = 0.0
+    y0, _ = _run(ctx, ws, x, ids, sc0, device=True)
+    ref0, _ = moe.moe_block(x, bank, ids, sc0, cache={})
+    assert np.max(np.abs(y0 - ref0)) <= 1e-3 * np.max(np.abs(ref0))
+    keep = [r for r in range(R) if r != 2]
+    assert np.array_equal(y0[keep].view(np.uint32), y[keep].view(np.uint32))
+    # invalid device routes -> NaN rows only
+    for bad in ("dup", "range", "neg", "nan"):
+        ib, sb = ids.copy(), sc.copy()
+        if bad == "dup":
+            ib[4, 2] = ib[4, 0]
+        elif bad == "range":
+            ib[4, 2] = 1000
+        elif bad == "neg":
+            sb[4, 2] = -1.0
+        else:
+            sb[4, 2] = np.nan
+        yb, _ = _run(ctx, ws, x, ib, sb, device=True)
+        assert np.isnan(yb[4]).all(), bad
+        others = [r for r in range(R) if r != 4]
+        assert np.array_equal(yb[others].view(np.uint32), y[others].view(np.uint32)), bad
+    # alpha / beta exactly on top of the same slot sum
+    old = synth.rng(5).standard_normal((R, I)).astype(np.float32)
+    yab, _ = _run(ctx, ws, x, ids, sc, alpha=0.75, beta=-1.5, old=old, device=True)
+    ref = (np.float32(0.75) * y).astype(np.float32)
+    ref = (ref + (np.float32(-1.5) * old).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(yab.view(np.uint32), ref.view(np.uint32))
+    _destroy(ws)
+
+
+def test_device_routes_rewritten_between_graph_replays(ctx):
+    E, I, H, R, k = 8, 256, 128, 4, 2
+    bank = synth.moe_bank(E, I, H, 2, 333)
+    ws = _weights(ctx, bank)
+    x = synth.activations(R, I, 334)
+    xd = _dev(x)
+    y = torch.empty((R, I), device=DEV)
+    routes = [synth.routes(R, E, k, 340 + i) for i in range(3)]
+    di = _dev(routes[0][0].astype(np.int32))
+    ds = _dev(routes[0][1])
+    stream = torch.cuda.Stream()
+    plan = runtime.MoePlan(ctx, ws, xd, y, device_ids=di, device_scores=ds, stream=stream)
+    expected = [_run(ctx, ws, x, i, s, device=True)[0] for i, s in routes]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        plan.submit()
+    torch.cuda.synchronize()
+    for rep in range(6):
+        i, s = routes[rep % 3]
+        di.copy_(_dev(i.astype(np.int32)))
+        ds.copy_(_dev(s))
+        torch.cuda.synchronize()
+        y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), expected[rep % 3].view(np.uint32)), rep
+    del graph
+    plan.destroy()
+    _destroy(ws)
+
+
+def test_staged_entry_points_and_validation(ctx):
+    E, I, H, R, k = 6, 256, 128, 2, 3
+    bank = synth.moe_bank(E, I, H, 2, 444)
+    ws = _weights(ctx, bank)
+    ids, sc = synth.routes(R, E, k, 445)
+    x = synth.activations(R, I, 446)
+    full, hidden = _run(ctx, ws, x, ids, sc, device=True)
+    y = torch.empty((R, I), device=DEV)
+    plan = runtime.MoePlan(ctx, ws, _dev(x), y, device_ids=_dev(ids.astype(np.int32)), device_scores=_dev(sc))
+    plan.gate_up()
+    plan.down()
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), full.view(np.uint32))
+    # weights retained by a plan cannot be destroyed
+    assert ctx.lib.strix_weights_destroy(ws[0][0].handle) != 0
+    plan.destroy()
+    # host routes must name exactly the given experts: 12 experts cannot all
+    # be used by 2 x 3 routes
+    wbig = _weights(ctx, synth.moe_bank(12, I, H, 2, 448))
+    with pytest.raises(abi.StrixError):
+        runtime.MoePlan(ctx, wbig, _dev(x), y, ids=ids, scores=sc)
+    # k > 8 routes per token is rejected
+    ids9, sc9 = synth.routes(1, 12, 9, 447)
+    with pytest.raises(abi.StrixError):
+        runtime.MoePlan(ctx, wbig, _dev(x[:1]), y[:1], device_ids=_dev(ids9.astype(np.int32)),
+                        device_scores=_dev(sc9))
+    _destroy(ws)
+    _destroy(wbig)

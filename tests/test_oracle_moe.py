@@ -1,0 +1,117 @@
+"""The routed-expert oracle: its exp and SwiGLU against FP64, and the block
+against its FP64 algebraic form and its structural identities."""
+import math
+
+import numpy as np
+import pytest
+
+import synth
+from oracle import linear, moe
+
+
+def _ulp_err(got, exact):
+    got = np.asarray(got, np.float64)
+    exact = np.asarray(exact, np.float64)
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    return np.abs(got - exact) / ulp
+
+
+def test_exp_constants_are_the_documented_splits():
+    assert float(moe.LN2_HEAD) == 0.693145751953125
+    # the head has at most 16 significant bits, so n * head is exact for |n| <= 256
+    m, _ = math.frexp(float(moe.LN2_HEAD))
+    assert (m * 2 ** 16).is_integer()
+    assert abs(float(moe.LN2_HEAD) + float(moe.LN2_TAIL) - math.log(2)) < 1e-13
+    assert moe.LOG2E.view(np.uint32) == 0x3FB8AA3B
+
+
+def test_exp_within_two_ulp_of_fp64():
+    x = np.concatenate([np.linspace(-87.0, 0.0, 400001, dtype=np.float64),
+                        -np.logspace(-30, 1.9, 20001)]).astype(np.float32)
+    got = moe.exp_nonpos(x)
+    exact = np.exp(x.astype(np.float64))
+    assert float(np.max(_ulp_err(got, exact))) <= 2.0
+    # subnormal results: absolute error within one subnormal step (2**-149) or two ulp
+    xs = np.linspace(-103.9, -87.5, 20001, dtype=np.float32)
+    err = np.abs(moe.exp_nonpos(xs).astype(np.float64) - np.exp(xs.astype(np.float64)))
+    assert float(np.max(err)) <= 2.0 * 2.0 ** -149 + 2e-7 * float(np.max(np.exp(xs.astype(np.float64))))
+
+
+def test_exp_special_values():
+    x = np.array([0.0, -0.0, -np.inf, np.nan, -104.5, -1e-45], np.float32)
+    got = moe.exp_nonpos(x)
+    assert got[0] == 1.0 and got[1] == 1.0 and got[2] == 0.0 and np.isnan(got[3]) and got[4] == 0.0
+    assert got[5] == 1.0
+
+
+def test_swiglu_against_fp64():
+    g = synth.rng(3).standard_normal(200000).astype(np.float32) * np.float32(6)
+    u = synth.rng(4).standard_normal(200000).astype(np.float32)
+    got = moe.swiglu(g, u).astype(np.float64)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    exact = g64 / (1.0 + np.exp(-g64)) * u64
+    # exp <= 2 ulp, one division, two products: a few ulp of the result
+    assert float(np.max(_ulp_err(got, exact))) <= 6.0
+    # sign symmetry of the stable form: sigmoid(-g) = 1 - sigmoid(g) is not
+    # assumed; SwiGLU(0, u) is exactly +0 or -0
+    assert np.all(moe.swiglu(np.zeros(4, np.float32), np.ones(4, np.float32)) == 0)
+
+
+def _tiny(K=2, E=5, I=256, H=128, R=3, k=2, seed=500, bias=True):
+    bank = synth.moe_bank(E, I, H, K, seed, bias=bias)
+    ids, sc = synth.routes(R, E, k, seed + 1)
+    x = synth.activations(R, I, seed + 2)
+    return bank, ids, sc, x
+
+
+def test_block_matches_fp64_algebraic_form():
+    bank, ids, sc, x = _tiny()
+    cache = {}
+    y, hidden = moe.moe_block(x, bank, ids, sc, cache=cache)
+    # FP64 algebraic reference: every projection through linear.matmul (FP64)
+    ref = np.zeros_like(y, dtype=np.float64)
+    for r in range(ids.shape[0]):
+        for s in range(ids.shape[1]):
+            e = bank[int(ids[r, s])]
+            lin = lambda v, w: linear.matmul(v, w[0], w[1], w[2], w[4], "mul1", w[3])
+            g = lin(x[r:r + 1].astype(np.float64), e["gate"])[0]
+            u = lin(x[r:r + 1].astype(np.float64), e["up"])[0]
+            h = g / (1.0 + np.exp(-g)) * u
+            ref[r] += float(sc[r, s]) * lin(h[None, :], e["down"])[0]
+    err = np.max(np.abs(y - ref)) / np.max(np.abs(ref))
+    assert err < 2e-3, err
+
+
+def test_block_identities():
+    bank, ids, sc, x = _tiny(R=4, k=3, E=6)
+    cache = {}
+    y, _ = moe.moe_block(x, bank, ids, sc, cache=cache)
+    # tokens are independent
+    y1, _ = moe.moe_block(x[2:3], bank, ids[2:3], sc[2:3], cache=cache)
+    assert np.array_equal(y1.view(np.uint32), y[2:3].view(np.uint32))
+    # a zero score contributes nothing: same bits as that slot's term absent
+    sc0 = sc.copy()
+    sc0[1, 2] = 0
+    y0, _ = moe.moe_block(x, bank, ids, sc0, cache=cache)
+    assert np.array_equal(y0[0].view(np.uint32), y[0].view(np.uint32))
+    assert not np.array_equal(y0[1], y[1])
+    # invalid tokens: repeated id, id outside the bank, negative or NaN score -> NaN row only
+    for bad in ("dup", "range", "neg", "nan"):
+        ib, sb = ids.copy(), sc.copy()
+        if bad == "dup":
+            ib[3, 1] = ib[3, 0]
+        elif bad == "range":
+            ib[3, 1] = len(bank)
+        elif bad == "neg":
+            sb[3, 1] = -0.5
+        else:
+            sb[3, 1] = np.nan
+        yb, _ = moe.moe_block(x, bank, ib, sb, cache=cache)
+        assert np.isnan(yb[3]).all()
+        assert np.array_equal(yb[:3].view(np.uint32), y[:3].view(np.uint32))
+    # alpha / beta on top of the same sum
+    old = synth.rng(9).standard_normal(y.shape).astype(np.float32)
+    yab, _ = moe.moe_block(x, bank, ids, sc, alpha=0.5, beta=-2.0, old=old, cache=cache)
+    ref = (np.float32(0.5) * y).astype(np.float32)
+    ref = (ref + (np.float32(-2.0) * old).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(yab.view(np.uint32), ref.view(np.uint32))
