@@ -9,6 +9,7 @@ Also reported on the same JSON line:
   sweep_gemv     decode GEMV, R = 1, 2, 4, 8 x {5120^2, 4096 -> 12288} x K4-6
   sweep_gemm     prefill GEMM, M = 128, 512, 2048 x the same shapes x K4-6
   grouped_o_a    16 groups x (4096 -> 1024) K5, R = 1..8, one grouped plan
+  moe_k2         64 experts (4096 <-> 1536, K2), 8 tokens, top-8, device routes
   roofline       the headline kernel: packed bytes / its mean launch time
   cpu_baseline   the NumPy oracle on the host cores, bounded sample
 
@@ -163,6 +164,67 @@ def bench_grouped(ctx, G, I, N, K, R, steps, warmup, seed):
             "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
 
 
+class MoeRotation:
+    """Copies of a whole expert bank, one device-route MoE plan each, all
+    reading the same device routes, x and y; one pass captured in a HIP graph."""
+
+    def __init__(self, ctx, E, I, H, K, R, k, seed, min_bytes=ROTATION_BYTES):
+        import numpy as np
+        import torch
+        import synth
+        from strix_trellis import runtime
+        bank = synth.moe_bank(E, I, H, K, seed)
+        ids, scores = synth.routes(R, E, k, seed + 1)
+        self.distinct = len(set(ids.ravel().tolist()))
+        per_expert = (2 * I * H + H * I) * K // 8
+        self.packed = self.distinct * per_expert
+        self.copies = max(2, -(-min_bytes // (E * per_expert)))
+        self.stream = torch.cuda.Stream()
+        self.x = torch.from_numpy(synth.activations(R, I, seed + 2)).to("cuda:0")
+        self.y = torch.empty((R, I), device="cuda:0")
+        self.ids = torch.from_numpy(ids.astype(np.int32)).to("cuda:0")
+        self.scores = torch.from_numpy(scores).to("cuda:0")
+        self.weights, self.plans = [], []
+        for _ in range(self.copies):
+            ws = [tuple(runtime.Weights(ctx, *e[p][:4], "mul1") for p in ("gate", "up", "down")) for e in bank]
+            self.weights.extend(w for t in ws for w in t)
+            self.plans.append(runtime.MoePlan(ctx, ws, self.x, self.y, device_ids=self.ids,
+                                              device_scores=self.scores, stream=self.stream))
+        torch.cuda.synchronize()
+        self.plans[0].submit()
+        torch.cuda.synchronize()
+        self.expected = self.y.clone()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            for p in self.plans:
+                p.submit()
+        torch.cuda.synchronize()
+
+    check = Rotation.check
+
+    def close(self):
+        del self.graph
+        for p in self.plans:
+            p.destroy()
+        for w in self.weights:
+            w.destroy()
+
+
+def bench_moe(ctx, steps, warmup, seed):
+    """C5: 64 experts (gate/up 4096 -> 1536, down 1536 -> 4096, K2), 8 tokens, top-8."""
+    E, I, H, K, R, k = 64, 4096, 1536, 2, 8, 8
+    rot = MoeRotation(ctx, E, I, H, K, R, k, seed)
+    try:
+        t = time_rotation(rot, steps, warmup)
+    finally:
+        rot.close()
+    gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
+    return {"experts": E, "I": I, "H": H, "K": K, "rows": R, "top_k": k, "distinct_experts": rot.distinct,
+            "packed_bytes": rot.packed, "us": round(t["ms"] * 1e3, 2), "packed_GBps": round(gbps, 1),
+            "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "launches": 2, "rotation_copies": rot.copies,
+            "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
+
+
 def cpu_baseline(sample_seconds=12.0):
     """NumPy oracle (decode + staged FP32 layer) on the north-star layer, host cores.
 
@@ -265,7 +327,7 @@ def main():
     head = bench_gemv(ctx, 4096, 4096, 4, 1, args.steps, args.warmup, synth.BASE_SEED)
     log(json.dumps(head))
     small_steps, small_warm = max(256, args.steps // 8), max(32, args.warmup // 8)
-    sweep, gemm, grouped = [], [], []
+    sweep, gemm, grouped, moe_cell = [], [], [], None
     if not args.quick:
         for (I, N) in ((5120, 5120), (4096, 12288)):
             for K in (4, 5, 6):
@@ -283,6 +345,8 @@ def main():
             cell = bench_grouped(ctx, 16, 4096, 1024, 5, R, small_steps, small_warm, synth.BASE_SEED + 3)
             log(json.dumps(cell))
             grouped.append(cell)
+        moe_cell = bench_moe(ctx, max(64, args.steps // 32), max(8, args.warmup // 32), synth.BASE_SEED + 4)
+        log(json.dumps(moe_cell))
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu:
         log(json.dumps(cpu))
@@ -313,6 +377,7 @@ def main():
         "sweep_gemv": sweep,
         "sweep_gemm": gemm,
         "grouped_o_a": grouped,
+        "moe_k2": moe_cell,
     }
     if gemm:
         best = {}

@@ -3,22 +3,31 @@
 
 namespace stx {
 
-__global__ __launch_bounds__(64) void input_stage_frag_kernel(const float* x, const uint16_t* suh, uint32_t M,
-                                                              uint32_t I, _Float16* afrag) {
-    const uint32_t blk = blockIdx.x, row = blockIdx.y;
-    const int lane = threadIdx.x;
-    const bool live = row < M;
+// Input stage of 16 rows x 128 channels into MFMA fragment order.  Each wave
+// stages four rows (one 128-block each) into an LDS tile; then every thread
+// writes one fragment lane: 8 consecutive channels of one row, 16 contiguous
+// bytes, so each fragment (64 lanes x 16 B) is one coalesced 1 KiB store.
+// Rows past M are zero.
+__global__ __launch_bounds__(256) void input_stage_frag_kernel(const float* x, const uint16_t* suh, uint32_t M,
+                                                               uint32_t I, _Float16* afrag) {
+    __shared__ __align__(16) _Float16 tile[16][128 + 8];
+    const uint32_t blk = blockIdx.x, rb = blockIdx.y;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint32_t ch = blk * 128;
-    const InputLoad l = input_load(x + (live ? uint64_t(row) * I : 0) + ch, suh + ch, live);
-    _Float16 v[2];
-    input_values(l, v[0], v[1]);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t k = ch + lane + 64 * h;
-        const uint32_t kb32 = k / 32, kk = k % 32;
-        const uint32_t fl = (row % 16) + 16 * (kk / 8);
-        afrag[afrag_offset(row / 16, kb32, I, fl) / 2 + (kk % 8)] = v[h];
+    for (int q = 0; q < 4; ++q) {
+        const int r = 4 * w + q;
+        const uint32_t row = rb * 16 + r;
+        const bool live = row < M;
+        const InputLoad l = input_load(x + (live ? uint64_t(row) * I : 0) + ch, suh + ch, live);
+        input_values(l, tile[r][lane], tile[r][lane + 64]);
     }
+    __syncthreads();
+    const int kb = tid >> 6;                 // 32-channel fragment within the 128 block
+    const int row = lane & 15, grp = lane >> 4;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[row][kb * 32 + grp * 8]);
+    u32x4* dst = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(afrag) + afrag_offset(rb, blk * 4 + kb, I, lane));
+    *(__attribute__((address_space(1))) u32x4*)(dst) = v;
 }
 
 // Rows per GEMM pass: the fragment buffer of one pass stays below 1 GiB so
@@ -67,8 +76,8 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         const uint64_t m = call.rows - r0 < pass ? call.rows - r0 : pass;
         const uint64_t mpad = (m + 15) / 16 * 16;
         const float* x = call.x + r0 * call.x_row_stride;
-        hipLaunchKernelGGL(input_stage_frag_kernel, dim3(w.input / 128, uint32_t(mpad)), dim3(64), 0, stream, x,
-                           w.suh, uint32_t(m), w.input, afrag);
+        hipLaunchKernelGGL(input_stage_frag_kernel, dim3(w.input / 128, uint32_t(mpad / 16)), dim3(256), 0, stream,
+                           x, w.suh, uint32_t(m), w.input, afrag);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         GemmLaunch l{};

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
     const GroupWeights gw = group_weights(a, z);
     float* y = a.y + z * a.y_group_stride;
     const float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
-    finish_columns<true>(a, gw, y, c, a.splits, [&](int s, int r) -> const float* {
+    finish_columns<true>(a, gw, column_operands(gw, c), y, c, a.splits, [&](int s, int r) -> const float* {
         return plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c;
     });
 }

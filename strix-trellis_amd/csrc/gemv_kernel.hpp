@@ -66,11 +66,34 @@ __device__ __forceinline__ float load_coherent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Output-stage operands of one lane's two columns (128c + lane, +64), loaded
+// ahead of the fold so their latency overlaps the completion round trip.
+constexpr int kFoldBatch = 16;
+
+struct ColumnOperands {
+    uint16_t sv0, sv1;
+    float b0, b1;
+};
+
+__device__ __forceinline__ ColumnOperands column_operands(const GroupWeights& gw, int c) {
+    const int lane = threadIdx.x & 63;
+    const int n0 = 128 * c + lane, n1 = n0 + 64;
+    ColumnOperands o;
+    o.sv0 = ld_global(gw.svh + n0);
+    o.sv1 = ld_global(gw.svh + n1);
+    o.b0 = gw.bias ? ld_global(gw.bias + n0) : 0.0f;
+    o.b1 = gw.bias ? ld_global(gw.bias + n1) : 0.0f;
+    return o;
+}
+
 // Output stage of column group c for every row: fold, H32, epilogue.
 // `plane(s, r)` returns the pointer to the 128 values of split s, row r.
+// The splits are folded in ascending order from +0; all their loads are
+// issued before the first add (one memory round trip per kFoldBatch splits):
+// a load past the last split re-reads the last plane and is not added.
 template <bool COHERENT, typename Plane>
-__device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWeights& gw, float* y, int c,
-                                               int splits, Plane plane) {
+__device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWeights& gw, const ColumnOperands& op,
+                                               float* y, int c, int splits, Plane plane) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     auto load = [](const float* p) -> float {
         if constexpr (COHERENT) return load_coherent(p);
@@ -78,47 +101,28 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
     };
     for (uint32_t r = w; r < a.rows; r += GEMV_WAVES) {
         float z0 = 0.0f, z1 = 0.0f;
-        int s = 0;
-        // Issue a batch of loads before the (ordered) adds that consume them:
-        // one memory round trip per 32 splits.
-        for (; s + 32 <= splits; s += 32) {
-            float v0[32], v1[32];
+        for (int s = 0; s < splits; s += kFoldBatch) {
+            float v0[kFoldBatch], v1[kFoldBatch];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                const float* p = plane(s + u, r);
+            for (int u = 0; u < kFoldBatch; ++u) {
+                const int ss = s + u < splits ? s + u : splits - 1;
+                const float* p = plane(ss, r);
                 v0[u] = load(p + lane);
                 v1[u] = load(p + lane + 64);
             }
 #pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                z0 = z0 + v0[u];
-                z1 = z1 + v1[u];
+            for (int u = 0; u < kFoldBatch; ++u) {
+                if (s + u < splits) {
+                    z0 = z0 + v0[u];
+                    z1 = z1 + v1[u];
+                }
             }
-        }
-        for (; s + 8 <= splits; s += 8) {
-            float v0[8], v1[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float* p = plane(s + u, r);
-                v0[u] = load(p + lane);
-                v1[u] = load(p + lane + 64);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                z0 = z0 + v0[u];
-                z1 = z1 + v1[u];
-            }
-        }
-        for (; s < splits; ++s) {
-            const float* p = plane(s, r);
-            z0 = z0 + load(p + lane);
-            z1 = z1 + load(p + lane + 64);
         }
         h32_wave(z0, z1);
         const int n0 = 128 * c + lane, n1 = n0 + 64;
         float* yr = y + r * a.y_row_stride;
-        const float o0 = output_element(z0, ld_global(gw.svh + n0), gw.bias, n0, a.alpha, a.beta, yr + n0);
-        const float o1 = output_element(z1, ld_global(gw.svh + n1), gw.bias, n1, a.alpha, a.beta, yr + n1);
+        const float o0 = output_value(z0, op.sv0, gw.bias != nullptr, op.b0, a.alpha, a.beta, yr + n0);
+        const float o1 = output_value(z1, op.sv1, gw.bias != nullptr, op.b1, a.alpha, a.beta, yr + n1);
         *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
         *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
     }
@@ -258,8 +262,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
         }
     }
     if (a.splits == 1) {
+        const ColumnOperands op = column_operands(gw, c);
         __syncthreads();
-        finish_columns<false>(a, gw, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
+        finish_columns<false>(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
         return;
     }
     if (a.mode == 0) return;
@@ -267,6 +272,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     // Single-launch completion: the last workgroup of column group (z, c)
     // finishes.  The coherent stores above are complete (waitcnt) before the
     // counter increment; the finishing loads are issued after it returned.
+    // The finisher's svh/bias loads go out with the partial stores: the wait
+    // below covers both, so the finisher starts with its operands in registers.
+    const ColumnOperands op = column_operands(gw, c);
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
@@ -278,7 +286,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     __syncthreads();
     if (!last_flag) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    finish_columns<true>(a, gw, y, c, a.splits, [&](int ss, int r) -> const float* {
+    finish_columns<true>(a, gw, op, y, c, a.splits, [&](int ss, int r) -> const float* {
         return plane_base + (uint64_t(ss) * a.rows + r) * a.N + 128 * c;
     });
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -152,6 +152,17 @@ __device__ __forceinline__ void moe_release() {
 
 constexpr int MOE_MAX_BPS = 32;
 constexpr int MOE_MAX_RT = 8;
+// Chunk loads in flight per wave and projection.  K2/K3 chunks are 8-12 bytes
+// per lane, so deep rings are what keeps enough bytes in flight per CU.
+constexpr int MOE_RING_GU = 4;
+constexpr int MOE_RING_D = 8;
+// LDS: the FP16 activations live until the main loop ends, the wave partials
+// only after it, so both share one buffer.
+constexpr int MOE_GU_ACT_BYTES = 2 * MOE_MAX_RT * MOE_MAX_BPS * 16 * 2;
+constexpr int MOE_GU_RED_BYTES = GEMV_WAVES * 2 * MOE_MAX_RT * 128 * 4;
+constexpr int MOE_D_ACT_BYTES = MOE_MAX_RT * MOE_MAX_BPS * 16 * 2;
+constexpr int MOE_D_RED_BYTES = GEMV_WAVES * MOE_MAX_RT * 128 * 4;
+constexpr int moe_max(int a, int b) { return a > b ? a : b; }
 
 // ---------------------------------------------------------------------------
 // Gate/up core of one workgroup: NP = 2 projections sharing the routed rows.
@@ -173,10 +184,10 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
     auto offg = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbg + og : kOut; };
     auto offu = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbu + ou : kOut; };
 
-    Chunk<KG> cg[2];
-    Chunk<KU> cu[2];
+    Chunk<KG> cg[MOE_RING_GU];
+    Chunk<KU> cu[MOE_RING_GU];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < MOE_RING_GU; ++u) {
         load_chunk(cg[u], rg, offg(u));
         load_chunk(cu[u], ru, offu(u));
     }
@@ -200,9 +211,9 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
 #pragma unroll
     for (int r = 0; r < RT; ++r) accg[r][0] = accg[r][1] = accu[r][0] = accu[r][1] = 0.0f;
     const bool first = g == 0;
-    for (int t = 0; t < nb; t += 2) {
+    for (int t = 0; t < nb; t += MOE_RING_GU) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < MOE_RING_GU; ++u) {
             if (t + u < nb) {
                 const int blk = w + GEMV_WAVES * (t + u);
                 half2_t wq[4][4];
@@ -213,10 +224,11 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
                 decode_chunk<KU, CB_MUL1>(cu[u], wq);
                 dot_block<RT>(wq, act + MOE_MAX_RT * act_row + blk * 16, act_row, accu);
             }
-            load_chunk(cg[u], rg, offg(t + u + 2));
-            load_chunk(cu[u], ru, offu(t + u + 2));
+            load_chunk(cg[u], rg, offg(t + u + MOE_RING_GU));
+            load_chunk(cu[u], ru, offu(t + u + MOE_RING_GU));
         }
     }
+    __syncthreads();   // every wave is done with act before red overwrites it
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         red[((w * 2 + 0) * MOE_MAX_RT + r) * 128 + 16 * jt + g] = accg[r][0];
@@ -229,8 +241,9 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
 
 template <int KG, int KU>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_gate_up_kernel(MoeArgs a) {
-    __shared__ __align__(16) _Float16 act[2 * MOE_MAX_RT * MOE_MAX_BPS * 16];
-    __shared__ __align__(16) float red[GEMV_WAVES * 2 * MOE_MAX_RT * 128];
+    __shared__ __align__(16) unsigned char lds[moe_max(MOE_GU_ACT_BYTES, MOE_GU_RED_BYTES)];
+    _Float16* act = reinterpret_cast<_Float16*>(lds);
+    float* red = reinterpret_cast<float*>(lds);
     __shared__ MoeGroup grp;
     __shared__ int last;
     const uint32_t c = blockIdx.x, route = blockIdx.y, split = blockIdx.z;
@@ -302,9 +315,9 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
     constexpr uint32_t kOut = 0x80000000u;
     auto off = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rb + lo : kOut; };
 
-    Chunk<K> ring[4];
+    Chunk<K> ring[MOE_RING_D];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) load_chunk(ring[u], rs, off(u));
+    for (int u = 0; u < MOE_RING_D; ++u) load_chunk(ring[u], rs, off(u));
 
     const int hblocks = int(bps) / 8, units = nrows * hblocks;
     for (int u = w; u < units; u += GEMV_WAVES) {
@@ -319,18 +332,19 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
 #pragma unroll
     for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
     const bool first = g == 0;
-    for (int t = 0; t < nb; t += 4) {
+    for (int t = 0; t < nb; t += MOE_RING_D) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < MOE_RING_D; ++u) {
             if (t + u < nb) {
                 half2_t wq[4][4];
                 link_chunk(ring[u], first);
                 decode_chunk<K, CB_MUL1>(ring[u], wq);
                 dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
             }
-            load_chunk(ring[u], rs, off(t + u + 4));
+            load_chunk(ring[u], rs, off(t + u + MOE_RING_D));
         }
     }
+    __syncthreads();   // every wave is done with act before red overwrites it
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         red[(w * MOE_MAX_RT + r) * 128 + 16 * jt + g] = acc[r][0];
@@ -341,8 +355,9 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
 
 template <int K>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_down_kernel(MoeArgs a) {
-    __shared__ __align__(16) _Float16 act[MOE_MAX_RT * MOE_MAX_BPS * 16];
-    __shared__ __align__(16) float red[GEMV_WAVES * MOE_MAX_RT * 128];
+    __shared__ __align__(16) unsigned char lds[moe_max(MOE_D_ACT_BYTES, MOE_D_RED_BYTES)];
+    _Float16* act = reinterpret_cast<_Float16*>(lds);
+    float* red = reinterpret_cast<float*>(lds);
     __shared__ MoeGroup grp;
     __shared__ uint32_t finish_mask;
     const uint32_t c = blockIdx.x, route = blockIdx.y, split = blockIdx.z;

@@ -92,4 +92,14 @@ __device__ __forceinline__ float output_element(float h, uint16_t svh, const flo
     return y;
 }
 
+// The same epilogue with svh bits and the bias value already loaded.
+__device__ __forceinline__ float output_value(float h, uint16_t svh, bool has_bias, float bias, float alpha,
+                                              float beta, const float* old) {
+    float y = rn32(h * half_bits_to_float(svh));
+    if (has_bias) y = rn32(y + bias);
+    y = rn32(y * alpha);
+    if (beta != 0.0f) y = rn32(y + rn32(beta * ld_global(old)));
+    return y;
+}
+
 }  // namespace stx
