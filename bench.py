@@ -279,18 +279,29 @@ def _traffic():
         return None
 
 
-def pmc_workload(ctx, launches):
-    """Fixed workload for counter passes: the headline plan over its rotation,
-    launched directly (no graph), then a plain 256 MiB device copy whose
-    FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes."""
+def pmc_workload(ctx, launches, which="gemv"):
+    """Fixed workload for counter passes, launched directly (no graph).
+
+    gemv: the headline plan over its rotation, then a plain 256 MiB device
+    copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters against known
+    bytes.  gemm: the M = 2048, 4096 -> 12288 K4 prefill plan.  moe: the C5
+    routed-expert plan."""
     import torch
     import synth
-    rot = Rotation(ctx, 4096, 4096, 4, 1, synth.BASE_SEED, "gemv")
+    if which == "moe":
+        rot = MoeRotation(ctx, 64, 4096, 1536, 2, 8, 8, synth.BASE_SEED + 4)
+    elif which == "gemm":
+        rot = Rotation(ctx, 4096, 12288, 4, 2048, synth.BASE_SEED + 2, "gemm")
+    else:
+        rot = Rotation(ctx, 4096, 4096, 4, 1, synth.BASE_SEED, "gemv")
     for i in range(launches):
         rot.plans[i % rot.copies].submit()
     torch.cuda.synchronize()
     ok = rot.check()
     rot.close()
+    if which != "gemv":
+        log(f"pmc workload {which}: {launches} launches (bit_identical={ok})")
+        return
     src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(4):
@@ -299,14 +310,37 @@ def pmc_workload(ctx, launches):
     log(f"pmc workload: {launches} headline launches (bit_identical={ok}), 4 copies of {src.numel() * 4} bytes")
 
 
+def run_section(ctx, which, steps, warmup):
+    """One section of the default run with the same cells and step counts."""
+    import synth
+    small_steps, small_warm = max(256, steps // 8), max(32, warmup // 8)
+    cells = []
+    if which == "gemv":
+        cells.append(bench_gemv(ctx, 4096, 4096, 4, 1, steps, warmup, synth.BASE_SEED))
+    elif which == "gemm":
+        for (I, N) in ((4096, 12288), (5120, 5120)):
+            for K in (4, 5, 6):
+                for M in (128, 512, 2048):
+                    cells.append(bench_gemm(ctx, M, I, N, K, 48, 8, synth.BASE_SEED + 2))
+    elif which == "grouped":
+        for R in range(1, 9):
+            cells.append(bench_grouped(ctx, 16, 4096, 1024, 5, R, small_steps, small_warm, synth.BASE_SEED + 3))
+    else:
+        cells.append(bench_moe(ctx, max(64, steps // 32), max(8, warmup // 32), synth.BASE_SEED + 4))
+    for c in cells:
+        print(json.dumps(c), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=4096)
     ap.add_argument("--warmup", type=int, default=512)
     ap.add_argument("--quick", action="store_true", help="headline only (no sweeps)")
+    ap.add_argument("--only", choices=("gemv", "gemm", "grouped", "moe"), default=None,
+                    help="run one section (for profiling); prints that section's cells only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--pmc-workload", action="store_true")
+    ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm", "moe"), default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (every box here has one MI355X); --gpus {args.gpus} "
@@ -320,7 +354,11 @@ def main():
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
     if args.pmc_workload:
-        pmc_workload(ctx, 256)
+        pmc_workload(ctx, {"gemv": 256, "gemm": 16, "moe": 16}[args.pmc_workload], args.pmc_workload)
+        return
+
+    if args.only:
+        run_section(ctx, args.only, args.steps, args.warmup)
         return
 
     log("headline: GEMV R1 K4 4096x4096")

@@ -3,31 +3,44 @@
 
 namespace stx {
 
-// Input stage of 16 rows x 128 channels into MFMA fragment order.  Each wave
-// stages four rows (one 128-block each) into an LDS tile; then every thread
-// writes one fragment lane: 8 consecutive channels of one row, 16 contiguous
-// bytes, so each fragment (64 lanes x 16 B) is one coalesced 1 KiB store.
-// Rows past M are zero.
+// Input stage of RB rows x 128 channels into MFMA A-fragment order: RB = 16
+// for the 16x32 fragments of gemm_kernel, RB = 32 for the 32x16 fragments of
+// gemm_wide_kernel.  Each wave stages RB / 4 rows (one 128-block each) into an
+// LDS tile; then every thread writes whole fragment lanes -- 8 consecutive
+// channels of one row, 16 contiguous bytes -- so each fragment (64 lanes x
+// 16 B) is one coalesced 1 KiB store.  Rows past M are zero.
+template <int RB>
 __global__ __launch_bounds__(256) void input_stage_frag_kernel(const float* x, const uint16_t* suh, uint32_t M,
                                                                uint32_t I, _Float16* afrag) {
-    __shared__ __align__(16) _Float16 tile[16][128 + 8];
+    __shared__ __align__(16) _Float16 tile[RB][128 + 8];
     const uint32_t blk = blockIdx.x, rb = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint32_t ch = blk * 128;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = 4 * w + q;
-        const uint32_t row = rb * 16 + r;
+    for (int q = 0; q < RB / 4; ++q) {
+        const int r = (RB / 4) * w + q;
+        const uint32_t row = rb * RB + r;
         const bool live = row < M;
         const InputLoad l = input_load(x + (live ? uint64_t(row) * I : 0) + ch, suh + ch, live);
         input_values(l, tile[r][lane], tile[r][lane + 64]);
     }
     __syncthreads();
-    const int kb = tid >> 6;                 // 32-channel fragment within the 128 block
-    const int row = lane & 15, grp = lane >> 4;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[row][kb * 32 + grp * 8]);
-    u32x4* dst = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(afrag) + afrag_offset(rb, blk * 4 + kb, I, lane));
-    *(__attribute__((address_space(1))) u32x4*)(dst) = v;
+#pragma unroll
+    for (int q = 0; q < RB / 16; ++q) {
+        const int fl = tid + 256 * q;
+        const int f = fl >> 6, l = fl & 63;        // fragment within the 128 block, its lane
+        uint64_t off;
+        u32x4 v;
+        if constexpr (RB == 16) {
+            v = *reinterpret_cast<const u32x4*>(&tile[l & 15][f * 32 + (l >> 4) * 8]);
+            off = afrag_offset(rb, blk * 4 + f, I, l);
+        } else {
+            v = *reinterpret_cast<const u32x4*>(&tile[l & 31][f * 16 + (l >> 5) * 8]);
+            off = afrag32_offset(rb, blk * 8 + f, I, l);
+        }
+        u32x4* dst = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(afrag) + off);
+        *(__attribute__((address_space(1))) u32x4*)(dst) = v;
+    }
 }
 
 // Rows per GEMM pass: the fragment buffer of one pass stays below 1 GiB so
@@ -44,7 +57,7 @@ static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
 uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
     const uint64_t pass = gemm_pass_rows(w);
     const uint64_t r = rows < pass ? rows : pass;
-    return align256(((r + 15) / 16) * 16 * w.input * 2);
+    return align256(((r + 31) / 32) * 32 * w.input * 2);   // rows padded for either fragment order
 }
 
 uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows) {
@@ -74,10 +87,18 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
     _Float16* afrag = static_cast<_Float16*>(call.workspace);
     for (uint64_t r0 = 0; r0 < call.rows; r0 += pass) {
         const uint64_t m = call.rows - r0 < pass ? call.rows - r0 : pass;
-        const uint64_t mpad = (m + 15) / 16 * 16;
+        // 256 x 256 tiles (32x16 fragments) once the rows fill them and N
+        // splits into 256-column blocks; 128-row tiles (16x32 fragments) otherwise.
+        const bool wide = m >= 256 && w.output % 256 == 0;
+        const uint32_t rb = wide ? 32 : 16;
+        const uint64_t mpad = (m + rb - 1) / rb * rb;
         const float* x = call.x + r0 * call.x_row_stride;
-        hipLaunchKernelGGL(input_stage_frag_kernel, dim3(w.input / 128, uint32_t(mpad / 16)), dim3(256), 0, stream,
-                           x, w.suh, uint32_t(m), w.input, afrag);
+        if (wide)
+            hipLaunchKernelGGL(input_stage_frag_kernel<32>, dim3(w.input / 128, uint32_t(mpad / 32)), dim3(256), 0,
+                               stream, x, w.suh, uint32_t(m), w.input, afrag);
+        else
+            hipLaunchKernelGGL(input_stage_frag_kernel<16>, dim3(w.input / 128, uint32_t(mpad / 16)), dim3(256), 0,
+                               stream, x, w.suh, uint32_t(m), w.input, afrag);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         GemmLaunch l{};
@@ -95,8 +116,6 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         l.codebook = w.codebook;
         l.bm = gemm_bm(m, w.output / 128);
         l.stream = stream;
-        // 256 x 256 tiles once the rows fill them (and N splits into 256-column blocks).
-        const bool wide = m >= 256 && w.output % 256 == 0;
         e = wide ? gemm_wide_table[w.bits - 1](l) : gemm_table[w.bits - 1](l);
         if (e != hipSuccess) return e;
     }

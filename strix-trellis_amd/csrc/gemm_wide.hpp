@@ -1,21 +1,30 @@
 // Prefill GEMM, wide variant for M >= 256: workgroup tile 256 x 256, eight
-// waves (two per SIMD) of 128 x 64, K stages of 64 channels.
+// waves (two per SIMD) of 128 x 64, K stages of 64 channels, built on
+// v_mfma_f32_32x32x16_f16.
 //
-// Measured on MI355X: v_mfma_f32_16x16x32_f16 reaches ~77% of peak with two
-// waves per SIMD but only ~51% with one; LDS reads run at ~150 B/clk/CU and
-// the vector-memory path at ~64 B/clk/CU.  So both operands are staged once
-// per workgroup in LDS (never re-read per wave from L2) and waves are 128 x 64
-// (operand bytes per flop 1/64 + 1/128 instead of 1/32 for 64 x 64).  Per stage:
-//   * A (256 rows x 64 channels, 32 KiB) is copied from the fragment-ordered
-//     core input in global memory into LDS through VGPRs, one stage ahead;
+// Measured on MI355X (independent accumulators, no memory traffic): the
+// 32x32x16 MFMA sustains ~2.1 PFLOP/s (85 % of the fp16 peak) with one or two
+// waves per SIMD, the 16x16x32 form only ~1.3-1.5 PFLOP/s; LDS reads run at
+// ~150 B/clk/CU.  So both operands are staged once per workgroup in LDS and
+// each wave computes a 128 x 64 block as 4 x 2 tiles of 32 x 32.  Per stage:
+//   * A (256 rows x 64 channels, 32 KiB) is DMA'd (buffer_load ... lds) from
+//     the 32x16 fragment-ordered core input straight into LDS, two stages
+//     ahead (three buffers);
 //   * B (64 x 256 = 4 input blocks x 16 tiles) is decoded from the trellis:
 //     wave w decodes block w / 2, tiles 8 (w % 2) .. +7, one chunk per lane,
-//     straight into MFMA B-fragment order in LDS; the raw chunks stream
-//     through a register ring 2 stages deep;
-//   * each wave runs 2 K32 steps x 8 x 4 v_mfma_f32_16x16x32_f16.
-// LDS: A and B double-buffered, 4 x 32 KiB; the epilogue reuses it as a
-// [128][256] FP32 tile (one half of the rows at a time) so each wave can run
-// H128 over whole 128-column groups.
+//     straight into 16x32 B-fragment order in LDS (double-buffered); the
+//     decode of stage st + 1 is interleaved with the MFMAs of stage st;
+//   * each wave runs 4 K16 steps x 4 x 2 v_mfma_f32_32x32x16_f16.
+// LDS: 3 A + 2 B buffers of 32 KiB; the epilogue reuses it as a [128][256]
+// FP32 tile (one half of the rows at a time) so each wave can run H128 over
+// whole 128-column groups.
+//
+// MFMA 32x32x16 f16 operand layout (lane l, e = 0..7, r = 0..15), checked on
+// the device:  A: A[l % 32][8 (l / 32) + e]   B: B[8 (l / 32) + e][l % 32]
+//              D: D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
+// Per output the K order is the MFMA K16 steps in ascending K from +0, as in
+// every other GEMM path here (the order inside one MFMA is the hardware's),
+// so rows have the same bits whichever tile computes them.
 #pragma once
 #include <type_traits>
 
@@ -23,16 +32,23 @@
 
 namespace stx {
 
-constexpr int WIDE_TILE_BYTES = 16 * 2 * 64 * 16;   // 16 fragment rows/tiles x 2 K32 x 64 lanes x 16 B
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr int WIDE_TILE_BYTES = 32 * 64 * 16;        // 32 fragments (8 x 4 K16) x 64 lanes x 16 B
 constexpr int WIDE_EPI_STRIDE = 260;                 // floats per staged row (256 + pad)
 constexpr size_t WIDE_LDS_BYTES =
     5 * size_t(WIDE_TILE_BYTES) > 128 * WIDE_EPI_STRIDE * 4 ? 5 * size_t(WIDE_TILE_BYTES) : 128 * WIDE_EPI_STRIDE * 4;
 
+// Byte offset of the 32 x 16 A fragment (32-row block rb, 16-channel block kb) of lane l.
+__host__ __device__ __forceinline__ uint64_t afrag32_offset(uint32_t rb, uint32_t kb, uint32_t I, uint32_t lane) {
+    return ((uint64_t(rb) * (I / 16) + kb) * 64 + lane) * 16;
+}
+
 template <int K, int CB>
 __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char* abuf = smem;                          // 3 x [16 rb][2 k32][64][16 B]
-    unsigned char* bbuf = smem + 3 * WIDE_TILE_BYTES;    // 2 x [16 tiles][2 k32][64][16 B]
+    unsigned char* abuf = smem;                          // 3 x [8 rb32][4 kb16][64][16 B]
+    unsigned char* bbuf = smem + 3 * WIDE_TILE_BYTES;    // 2 x [8 n32][4 kb16][64][16 B]
     const int c = blockIdx.x, mb = blockIdx.y;           // c: 256-column block
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wm = w >> 2, wn = w & 3;
@@ -52,16 +68,17 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     auto load_stage = [&](Chunk<K>& dst, uint32_t st) {
         load_chunk(dst, wrsrc, st < stages ? (st * 4 + dblk) * row_bytes + lane_off : 0x80000000u);
     };
+    // Lane (tile dtile, chunk g) holds rows 0..15 of tile columns g and g+8 of
+    // input block dblk: column n = 16 (dtile % 2) + g (+8) of 32-column block
+    // dtile / 2; rows 0..7 go to fragment lane n, rows 8..15 to lane 32 + n.
     auto store_bfrag = [&](const half2_t (&wq)[4][4], int buf) {
-        unsigned char* base = bbuf + buf * WIDE_TILE_BYTES;
-        const int k32 = dblk >> 1, kg = (dblk & 1) * 2;
-        auto frag = [&](int n, int kgroup) -> u32x4* {
-            return reinterpret_cast<u32x4*>(base + ((dtile * 2 + k32) * 64 + kgroup * 16 + n) * 16);
-        };
-        *frag(g, kg) = u32x4{as_u32(wq[0][0]), as_u32(wq[1][0]), as_u32(wq[2][0]), as_u32(wq[3][0])};
-        *frag(g, kg + 1) = u32x4{as_u32(wq[0][1]), as_u32(wq[1][1]), as_u32(wq[2][1]), as_u32(wq[3][1])};
-        *frag(g + 8, kg) = u32x4{as_u32(wq[0][2]), as_u32(wq[1][2]), as_u32(wq[2][2]), as_u32(wq[3][2])};
-        *frag(g + 8, kg + 1) = u32x4{as_u32(wq[0][3]), as_u32(wq[1][3]), as_u32(wq[2][3]), as_u32(wq[3][3])};
+        unsigned char* base = bbuf + buf * WIDE_TILE_BYTES + ((dtile >> 1) * 4 + dblk) * 1024;
+        const int n = 16 * (dtile & 1) + g;
+        auto frag = [&](int l) -> u32x4* { return reinterpret_cast<u32x4*>(base + l * 16); };
+        *frag(n) = u32x4{as_u32(wq[0][0]), as_u32(wq[1][0]), as_u32(wq[2][0]), as_u32(wq[3][0])};
+        *frag(32 + n) = u32x4{as_u32(wq[0][1]), as_u32(wq[1][1]), as_u32(wq[2][1]), as_u32(wq[3][1])};
+        *frag(n + 8) = u32x4{as_u32(wq[0][2]), as_u32(wq[1][2]), as_u32(wq[2][2]), as_u32(wq[3][2])};
+        *frag(40 + n) = u32x4{as_u32(wq[0][3]), as_u32(wq[1][3]), as_u32(wq[2][3]), as_u32(wq[3][3])};
     };
     auto decode_stage = [&](Chunk<K>& src, int buf) {
         link_chunk(src, g == 0);
@@ -70,18 +87,18 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         store_bfrag(wq, buf);
     };
 
-    // ---- A: wave w DMAs fragments 4w..4w+3 (fragment f = row block f/2, K32 step f%2)
-    // of a stage straight into LDS (buffer_load ... lds).  Three A buffers:
-    // stage st is issued two stages ahead, into buffer st % 3.
+    // ---- A: wave w DMAs fragments 4w..4w+3 (fragment f = 32-row block f/4,
+    // K16 step f%4) of a stage straight into LDS (buffer_load ... lds).  Three
+    // A buffers: stage st is issued two stages ahead, into buffer st % 3.
     auto dma_a = [&](uint32_t st) {
-        const uint32_t kb = st < stages ? 2 * st : 0;
+        const uint32_t kb = st < stages ? 4 * st : 0;
         unsigned char* base = abuf + (st % 3) * WIDE_TILE_BYTES;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int f = 4 * w + q;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 arsrc, (__attribute__((address_space(3))) void*)(base + f * 1024), 16,
-                uint32_t(afrag_offset(uint32_t(mb) * 16 + (f >> 1), kb + (f & 1), I, lane)), 0, 0, 0);
+                uint32_t(afrag32_offset(uint32_t(mb) * 8 + (f >> 2), kb + (f & 3), I, lane)), 0, 0, 0);
         }
     };
     // The compiler does not see the LDS side of these loads, so their
@@ -100,15 +117,15 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(v) : "memory");
     };
 
-    float4_t acc[8][4];
+    float16_t acc[4][2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 2; ++j) acc[i][j] = float16_t{};
 
     // Prologue: A stages 0 and 1 in flight, B stage 0 decoded, chunk ring full.
-    load_stage(ring[0], 0);
-    load_stage(ring[1], 1);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_stage(ring[d], d);
     __builtin_amdgcn_sched_barrier(0);
     dma_a(0);
     dma_a(1);
@@ -126,13 +143,10 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             dma_a(st + 2);
             __builtin_amdgcn_sched_barrier(0);
             // One instruction stream per stage: the MFMAs of stage st and the
-            // VALU decode of stage st + 1 are independent, and they are
-            // interleaved in source order -- one weight pair decoded after
-            // every 4 MFMAs -- so the matrix core and the VALU work at the
-            // same time (issued as two phases they take turns: both waves of
-            // a SIMD move in lockstep between barriers).  The decoder's inline
-            // v_mad_u32_u16 pins the order for the machine scheduler.
-            // stages = I / 64 is even, so every unrolled stage is live.
+            // VALU decode of stage st + 1 are independent and interleaved in
+            // source order (one weight pair after every two MFMAs), so the
+            // matrix core and the VALU work at the same time.  The decoder's
+            // inline v_mad_u32_u16 pins the order for the machine scheduler.
             const unsigned char* ab = abuf + (st % 3) * WIDE_TILE_BYTES;
             const unsigned char* bb = bbuf + (st & 1) * WIDE_TILE_BYTES;
             const int slot = (d + 1) % D;   // compile-time after unrolling
@@ -140,19 +154,20 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             link_chunk(dc, g == 0);
             half2_t wq[4][4];
 #pragma unroll
-            for (int k32 = 0; k32 < 2; ++k32) {
-                half8_t bf[4];
+            for (int kb = 0; kb < 4; ++kb) {
+                half8_t bf[2], af[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    bf[j] = *reinterpret_cast<const half8_t*>(bb + (((4 * wn + j) * 2 + k32) * 64 + lane) * 16);
+                for (int j = 0; j < 2; ++j)
+                    bf[j] = *reinterpret_cast<const half8_t*>(bb + (((2 * wn + j) * 4 + kb) * 64 + lane) * 16);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const half8_t af =
-                        *reinterpret_cast<const half8_t*>(ab + (((8 * wm + i) * 2 + k32) * 64 + lane) * 16);
+                for (int i = 0; i < 4; ++i)
+                    af[i] = *reinterpret_cast<const half8_t*>(ab + (((4 * wm + i) * 4 + kb) * 64 + lane) * 16);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
-                    decode_pair_at<K, CB>(dc, wq, 8 * k32 + i);
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    decode_pair_at<K, CB>(dc, wq, 4 * kb + i);
                 }
             }
             // Decoded stage st + 1 -> the other B buffer (past the end: zeros
@@ -168,36 +183,41 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     }
 
     // ---- Epilogue: rows [128 p, +128) through an LDS [128][256] FP32 tile ----
+    // A wave always finishes column group w % 2 of its rows, so its svh and
+    // bias operands are loaded once, ahead of the first pass.
+    const int grp = w & 1;
+    const uint32_t n0 = 256u * c + 128u * grp + lane, n1 = n0 + 64;
+    const uint16_t sv0 = ld_global(a.svh + n0), sv1 = ld_global(a.svh + n1);
+    const bool has_bias = a.bias != nullptr;
+    const float b0 = has_bias ? ld_global(a.bias + n0) : 0.0f, b1 = has_bias ? ld_global(a.bias + n1) : 0.0f;
     float* tile = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         if (wm == p) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int row = 16 * i + 4 * (lane >> 4) + e;
-                        const int col = 64 * wn + 16 * j + (lane & 15);
-                        tile[row * WIDE_EPI_STRIDE + col] = acc[i][j][e];
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        const int col = 64 * wn + 32 * j + (lane & 31);
+                        tile[row * WIDE_EPI_STRIDE + col] = acc[i][j][r];
                     }
         }
         __syncthreads();
-        // 128 rows x 2 column groups; a wave takes one (row, group) at a time.
-        for (int u = w; u < 256; u += 8) {
-            const int rr = u >> 1, grp = u & 1;
+        // 128 rows x 2 column groups; wave w takes rows w/2, w/2 + 4, ... of group w % 2.
+        for (int rr = w >> 1; rr < 128; rr += 4) {
             const uint32_t row = uint32_t(mb) * 256 + 128 * p + rr;
             float z0 = tile[rr * WIDE_EPI_STRIDE + 128 * grp + lane];
             float z1 = tile[rr * WIDE_EPI_STRIDE + 128 * grp + lane + 64];
             h32_wave(z0, z1);
             if (row < a.M) {
-                const uint32_t n0 = 256u * c + 128u * grp + lane, n1 = n0 + 64;
                 float* yr = a.y + uint64_t(row) * N;
-                const float o0 = output_element(z0, ld_global(a.svh + n0), a.bias, n0, a.alpha, a.beta, yr + n0);
-                const float o1 = output_element(z1, ld_global(a.svh + n1), a.bias, n1, a.alpha, a.beta, yr + n1);
-                yr[n0] = o0;
-                yr[n1] = o1;
+                const float o0 = output_value(z0, sv0, has_bias, b0, a.alpha, a.beta, yr + n0);
+                const float o1 = output_value(z1, sv1, has_bias, b1, a.alpha, a.beta, yr + n1);
+                *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+                *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
             }
         }
         __syncthreads();

@@ -21,16 +21,48 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
     return (float)__builtin_bit_cast(_Float16, bits);
 }
 
-__device__ __forceinline__ void h32_wave(float& v0, float& v1) {
+// v of lane l ^ S, without the LDS crossbar: DPP quad permutes for strides 1
+// and 2, row shifts for 4, a row rotate for 8, and the gfx950 permlane swaps
+// (odd/even 16-lane rows, upper/lower 32-lane halves) for 16 and 32.
+template <int S>
+__device__ __forceinline__ float xor_lane(float v) {
     const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int stride = 1; stride < 64; stride <<= 1) {
-        const float p0 = __shfl_xor(v0, stride, 64);
-        const float p1 = __shfl_xor(v1, stride, 64);
-        const bool upper = (lane & stride) != 0;
-        v0 = upper ? p0 - v0 : v0 + p0;
-        v1 = upper ? p1 - v1 : v1 + p1;
+    const int iv = __builtin_bit_cast(int, v);
+    if constexpr (S == 1) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+    } else if constexpr (S == 2) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+    } else if constexpr (S == 4) {
+        const int up = __builtin_amdgcn_mov_dpp(iv, 0x104, 0xf, 0xf, false);     // row_shl:4 -> lane + 4
+        const int down = __builtin_amdgcn_mov_dpp(iv, 0x114, 0xf, 0xf, false);   // row_shr:4 -> lane - 4
+        return __builtin_bit_cast(float, (lane & 4) ? down : up);
+    } else if constexpr (S == 8) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x128, 0xf, 0xf, false));  // row_ror:8
+    } else if constexpr (S == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(uint32_t(iv), uint32_t(iv), false, false);
+        return __builtin_bit_cast(float, (lane & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(S == 32, "lane exchange stride");
+        const auto r = __builtin_amdgcn_permlane32_swap(uint32_t(iv), uint32_t(iv), false, false);
+        return __builtin_bit_cast(float, (lane & 32) ? r[0] : r[1]);
     }
+}
+
+template <int S>
+__device__ __forceinline__ void butterfly(float& v0, float& v1) {
+    const bool upper = (threadIdx.x & S) != 0;
+    const float p0 = xor_lane<S>(v0), p1 = xor_lane<S>(v1);
+    v0 = upper ? p0 - v0 : v0 + p0;
+    v1 = upper ? p1 - v1 : v1 + p1;
+}
+
+__device__ __forceinline__ void h32_wave(float& v0, float& v1) {
+    butterfly<1>(v0, v1);
+    butterfly<2>(v0, v1);
+    butterfly<4>(v0, v1);
+    butterfly<8>(v0, v1);
+    butterfly<16>(v0, v1);
+    butterfly<32>(v0, v1);
     const float a = v0, b = v1;
     v0 = rn32(a + b);
     v1 = rn32(a - b);
