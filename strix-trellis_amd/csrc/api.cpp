@@ -512,8 +512,9 @@ strix_status strix_gemm(strix_context c, const strix_matmul_desc* d, const strix
 }
 
 // Plans: validated once; a GEMV plan with split partials runs as one launch
-// with completion counters owned by the weights, so captured graphs stay valid
-// after the plan is destroyed (reference src/api.hip:505-563, docs/API.md:230-295).
+// on dedicated partial planes owned by the weights (the reference keeps its
+// completion counters there), so captured graphs stay valid after the plan is
+// destroyed (reference src/api.hip:505-563, docs/API.md:230-295).
 strix_status strix_linear_plan_create(strix_context c, const strix_matmul_desc* d, const strix_stream* stream,
                                       uint32_t operation, strix_linear_plan* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
@@ -541,15 +542,15 @@ strix_status strix_linear_plan_create(strix_context c, const strix_matmul_desc* 
     plan->gemm = gemm;
     plan->call = make_call(*d, call.rows, d->workspace);
     plan->launches = 0;
-    const uint32_t counters = (!gemm && call.rows) ? stx::gemv_counter_count(w->dev) : 0;
-    if (counters) {
+    const uint64_t words = (!gemm && call.rows) ? stx::gemv_plane_words(w->dev, call.rows) : 0;
+    if (words) {
         void* p = nullptr;
-        hipError_t e = hipMalloc(&p, counters * sizeof(uint32_t));
-        if (e == hipSuccess) e = stx::launch_fill_u32(static_cast<uint32_t*>(p), 0, counters, hs);
+        hipError_t e = hipMalloc(&p, words * sizeof(uint32_t));
+        if (e == hipSuccess) e = stx::launch_fill_u32(static_cast<uint32_t*>(p), stx::GEMV_PLANE_EMPTY, words, hs);
         if (e == hipSuccess) e = hipStreamSynchronize(hs);
         if (e == hipSuccess) {
             try {
-                w->counter_arrays.push_back(p);
+                w->counter_arrays.push_back(p);   // freed with the weights
             } catch (...) {
                 e = hipErrorOutOfMemory;
             }
@@ -559,9 +560,9 @@ strix_status strix_linear_plan_create(strix_context c, const strix_matmul_desc* 
             delete plan;
             return from_hip(e);
         }
-        plan->counters = static_cast<uint32_t*>(p);
+        plan->planes = static_cast<float*>(p);
     }
-    if (call.rows) plan->launches = stx::linear_launch_count(w->dev, call.rows, gemm, plan->counters != nullptr);
+    if (call.rows) plan->launches = stx::linear_launch_count(w->dev, call.rows, gemm, plan->planes != nullptr);
     ++w->plans;
     *out = plan;
     return STRIX_SUCCESS;
@@ -572,7 +573,7 @@ strix_status strix_linear_plan_submit(strix_linear_plan p) {
     const strix_status s = context_ok(p->owner);
     if (s != STRIX_SUCCESS || !p->call.rows) return s;
     const stx::DeviceWeights& w = p->weights->dev;
-    if (!p->gemm && p->counters) return from_hip(stx::launch_gemv_fused(w, p->call, p->counters, p->stream));
+    if (!p->gemm && p->planes) return from_hip(stx::launch_gemv_fused(w, p->call, p->planes, p->stream));
     return from_hip(stx::launch_linear(w, p->call, p->gemm, p->stream));
 }
 

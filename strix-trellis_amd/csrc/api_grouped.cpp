@@ -7,9 +7,10 @@
 // group), so each row has exactly the bits of that row submitted alone through
 // strix_gemv (STRIX_GEMV_ROW_INVARIANT_R1).  Workspace layout, all offsets a
 // function of the geometry only:
-//   [counters: kMaxGroups * N/128 u32][group table: kMaxGroups entries][partials: G * S * rows * N f32]
-// Creation uploads the table, zeroes the counters and synchronises the stream;
-// each completed submission leaves the counters zero again.
+//   [group table: kMaxGroups entries][partials: G * S * rows * N f32]
+// The workspace is dedicated to the plan: creation uploads the table, fills
+// the partial planes with GEMV_PLANE_EMPTY and synchronises the stream; each
+// completed submission leaves the planes EMPTY again (one launch per submit).
 #include "api_internal.hpp"
 
 #include <new>
@@ -22,7 +23,7 @@ constexpr uint64_t kAlign = STRIX_TRELLIS_WORKSPACE_ALIGNMENT;
 uint64_t align_up(uint64_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
 struct GroupLayout {
-    uint64_t counter_bytes = 0, table_offset = 0, partial_offset = 0, bytes = 0;
+    uint64_t table_offset = 0, partial_offset = 0, plane_words = 0, bytes = 0;
 };
 
 struct Validated {
@@ -81,11 +82,10 @@ strix_status validate(strix_context c, const strix_grouped_gemv_desc* d, Validat
             return STRIX_ERROR_INVALID_ARGUMENT;
     const stx::GemvShape sh = stx::gemv_shape(uint32_t(I), uint32_t(N), v.geometry.bits);
     GroupLayout& L = v.layout;
-    L.counter_bytes = (N / 128) * 4;
-    L.table_offset = align_up(kMaxGroups * L.counter_bytes);
-    L.partial_offset = L.table_offset + align_up(kMaxGroups * sizeof(stx::GroupWeights));
-    const uint64_t planes = sh.splits > 1 ? uint64_t(sh.splits) * rows * N * 4 : 0;
-    L.bytes = L.partial_offset + align_up(planes * G);
+    L.table_offset = 0;
+    L.partial_offset = align_up(kMaxGroups * sizeof(stx::GroupWeights));
+    L.plane_words = sh.splits > 1 ? uint64_t(sh.splits) * rows * N * G : 0;
+    L.bytes = L.partial_offset + align_up(L.plane_words * 4);
     return STRIX_SUCCESS;
 }
 }  // namespace
@@ -96,7 +96,6 @@ struct strix_grouped_gemv_plan_impl {
     stx::DeviceWeights geometry{};
     stx::LinearCall call{};
     const stx::GroupWeights* table = nullptr;
-    uint32_t* counters = nullptr;
     uint64_t xgs = 0, ygs = 0;
     hipStream_t stream{};
 };
@@ -149,12 +148,13 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
         return STRIX_ERROR_OUT_OF_MEMORY;
     }
     char* base = static_cast<char*>(d->workspace);
-    p->counters = reinterpret_cast<uint32_t*>(base);
+
     p->table = reinterpret_cast<const stx::GroupWeights*>(base + v.layout.table_offset);
     hipError_t e = hipMemcpyAsync(base + v.layout.table_offset, table.data(), table.size() * sizeof(table[0]),
                                   hipMemcpyHostToDevice, hs);
     if (e == hipSuccess)
-        e = stx::launch_fill_u32(p->counters, 0, v.layout.counter_bytes / 4 * v.weights.size(), hs);
+        e = stx::launch_fill_u32(reinterpret_cast<uint32_t*>(base + v.layout.partial_offset), stx::GEMV_PLANE_EMPTY,
+                                 v.layout.plane_words, hs);
     const hipError_t done = hipStreamSynchronize(hs);
     if (e != hipSuccess || done != hipSuccess) {
         delete p;
@@ -183,7 +183,7 @@ strix_status strix_grouped_gemv_plan_submit(strix_grouped_gemv_plan p) {
     const strix_status s = context_ok(p->owner);
     if (s != STRIX_SUCCESS) return s;
     return from_hip(stx::launch_gemv_grouped(p->geometry, p->table, uint32_t(p->retained.size()), p->call, p->xgs,
-                                             p->ygs, p->counters, p->stream));
+                                             p->ygs, true, p->stream));
 }
 
 strix_status strix_grouped_gemv_plan_destroy(strix_grouped_gemv_plan p) {

@@ -19,7 +19,7 @@ struct strix_weights_impl {
     void* base = nullptr;     // single private allocation: trellis | suh | svh | bias
     uint64_t bytes = 0;
     uint64_t plans = 0;       // live plans retaining these weights
-    // Completion-counter arrays of plans created on these weights.  Graphs
+    // Single-launch state (partial planes) of plans created on these weights.  Graphs
     // captured from a plan may replay after the plan is destroyed, so the
     // arrays live until the weights are destroyed.
     std::vector<void*> counter_arrays;
@@ -31,7 +31,7 @@ struct strix_linear_plan_impl {
     stx::LinearCall call{};
     hipStream_t stream{};
     bool gemm = false;
-    uint32_t* counters = nullptr;
+    float* planes = nullptr;    // dedicated split planes of the single-launch GEMV
     uint32_t launches = 0;
 };
 

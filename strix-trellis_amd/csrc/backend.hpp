@@ -41,8 +41,11 @@ GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t bits);
 uint64_t gemv_workspace_bytes(const DeviceWeights& w, uint32_t rows);
 uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows);
 uint64_t linear_workspace_bytes(const DeviceWeights& w, uint64_t rows);
-// Completion counters (u32) a single-launch GEMV needs: one per 128 outputs.
-uint32_t gemv_counter_count(const DeviceWeights& w);
+// Single-launch GEMV: F32 words of the dedicated partial planes a plan owns
+// ([splits][rows][N], 0 when one split suffices).  Between launches every word
+// holds GEMV_PLANE_EMPTY.
+constexpr uint32_t GEMV_PLANE_EMPTY = 0xFFFFFFFFu;
+uint64_t gemv_plane_words(const DeviceWeights& w, uint64_t rows);
 
 struct LinearCall {
     const float* x = nullptr;
@@ -57,19 +60,21 @@ struct LinearCall {
 
 // Generic GEMV (rows 1..8): core kernel + finishing kernel, no counters.
 hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
-// Single-launch GEMV: the last workgroup of each 128-output group finishes.
-// `counters` must be zero on entry; they are zero again when the launch ends.
-hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, uint32_t* counters,
-                             hipStream_t stream);
+// Single-launch GEMV: the workgroup of the last split of each 128-output group
+// waits for the other splits' planes and finishes.  `planes` must hold
+// GEMV_PLANE_EMPTY in every word on entry and does again when the launch ends.
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, float* planes, hipStream_t stream);
 // Grouped GEMV over `groups` weights of one geometry (table in device memory).
+// single_launch: the planes are call.workspace, dedicated and EMPTY-filled as
+// for launch_gemv_fused; otherwise a finishing kernel folds them.
 hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
                                const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
-                               uint32_t* counters, hipStream_t stream);
+                               bool single_launch, hipStream_t stream);
 // Prefill path (any row count): input stage to FP16 in the workspace, then the
 // MFMA core with the fused output stage.
 hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
 uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows);
-uint32_t linear_launch_count(const DeviceWeights& w, uint64_t rows, bool gemm, bool counters);
+uint32_t linear_launch_count(const DeviceWeights& w, uint64_t rows, bool gemm, bool single_launch);
 // Dispatch used by strix_gemv / strix_gemm / grouped MoE.
 hipError_t launch_linear(const DeviceWeights& w, const LinearCall& call, bool prefer_gemm, hipStream_t stream);
 

@@ -15,10 +15,10 @@ uint64_t linear_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
     return gemv > gemm ? gemv : gemm;
 }
 
-uint32_t linear_launch_count(const DeviceWeights& w, uint64_t rows, bool gemm, bool counters) {
+uint32_t linear_launch_count(const DeviceWeights& w, uint64_t rows, bool gemm, bool single_launch) {
     if (!rows) return 0;
     if (gemm || rows > 8) return gemm_launch_count(w, rows);
-    if (counters) return 1;
+    if (single_launch) return 1;
     return gemv_shape(w.input, w.output, w.bits).splits > 1 ? 2 : 1;
 }
 

@@ -31,9 +31,9 @@ uint64_t gemv_workspace_bytes(const DeviceWeights& w, uint32_t rows) {
     return align256(uint64_t(sh.splits) * rows * w.output * sizeof(float));
 }
 
-uint32_t gemv_counter_count(const DeviceWeights& w) {
+uint64_t gemv_plane_words(const DeviceWeights& w, uint64_t rows) {
     const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
-    return sh.splits > 1 ? w.output / 128 : 0;
+    return sh.splits > 1 ? uint64_t(sh.splits) * rows * w.output : 0;
 }
 
 static uint32_t rows_template(uint64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
 }
 
 static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table, uint32_t groups,
-                              const LinearCall& call, uint64_t xg, uint64_t yg, uint32_t* counters,
+                              const LinearCall& call, uint64_t xg, uint64_t yg, float* planes,
                               uint32_t mode, hipStream_t stream) {
     const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
     GemvLaunch l{};
@@ -63,8 +63,7 @@ static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table,
     a.table = table;
     a.x = call.x;
     a.y = call.y;
-    a.partials = static_cast<float*>(call.workspace);
-    a.counters = counters;
+    a.partials = planes;
     a.x_row_stride = call.x_row_stride;
     a.y_row_stride = call.y_row_stride;
     a.x_group_stride = xg;
@@ -94,28 +93,27 @@ static bool gemv_fits(const DeviceWeights& w) {
 
 hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream) {
     if (!gemv_fits(w)) return hipErrorInvalidValue;
-    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, nullptr, 0, stream);
+    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, static_cast<float*>(call.workspace), 0, stream);
     hipError_t e = gemv_table[w.bits - 1](l);
     if (e != hipSuccess || l.args.splits == 1) return e;
     hipLaunchKernelGGL(gemv_finish_kernel, dim3(w.output / 128, 1, 1), dim3(GEMV_THREADS), 0, stream, l.args);
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, uint32_t* counters,
-                             hipStream_t stream) {
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, float* planes, hipStream_t stream) {
     if (!gemv_fits(w)) return hipErrorInvalidValue;
-    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, counters, 1, stream);
+    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, planes, 1, stream);
     return gemv_table[w.bits - 1](l);
 }
 
 hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
                                const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
-                               uint32_t* counters, hipStream_t stream) {
+                               bool single_launch, hipStream_t stream) {
     if (!gemv_fits(geometry)) return hipErrorInvalidValue;
-    GemvLaunch l = make_launch(geometry, table, groups, call, x_group_stride, y_group_stride, counters,
-                               counters ? 1 : 0, stream);
+    GemvLaunch l = make_launch(geometry, table, groups, call, x_group_stride, y_group_stride,
+                               static_cast<float*>(call.workspace), single_launch ? 1 : 0, stream);
     hipError_t e = gemv_table[geometry.bits - 1](l);
-    if (e != hipSuccess || counters || l.args.splits == 1) return e;
+    if (e != hipSuccess || single_launch || l.args.splits == 1) return e;
     hipLaunchKernelGGL(gemv_finish_kernel, dim3(geometry.output / 128, 1, groups), dim3(GEMV_THREADS), 0,
                        stream, l.args);
     return hipGetLastError();

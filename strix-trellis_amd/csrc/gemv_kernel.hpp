@@ -18,9 +18,9 @@
 //   * the four waves' partial sums meet in LDS and are added in wave order;
 //   * S == 1: the workgroup applies the output stage itself.  Otherwise it
 //     writes its [rows][128] partial plane; the finishing step (a second
-//     kernel, or with completion counters the last-arriving workgroup of the
-//     column group) folds the S planes in ascending split order from +0 and
-//     applies the output stage.
+//     kernel, or in a single-launch plan the workgroup of split S-1, which
+//     waits for the other planes) folds the S planes in ascending split order
+//     from +0 and applies the output stage.
 //
 // Per-output accumulation order (defines the core's bits; depends on I, N,
 // K only, never on the row count):
@@ -43,12 +43,11 @@ struct GemvArgs {
     const float* x;
     float* y;
     float* partials;              // [groups][S][rows][N]
-    uint32_t* counters;           // [groups][N/128]
     uint64_t x_row_stride, y_row_stride;
     uint64_t x_group_stride, y_group_stride;
     uint32_t I, N, rows, splits, bps;
     float alpha, beta;
-    uint32_t mode;                // 0: partial planes only, 1: last workgroup finishes
+    uint32_t mode;                // 0: partial planes only, 1: the last split finishes
 };
 
 __device__ __forceinline__ GroupWeights group_weights(const GemvArgs& a, int z) {
@@ -128,6 +127,73 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
     }
 }
 
+// Single-launch completion without a counter.  The planes are dedicated to
+// the plan and hold GEMV_PLANE_EMPTY between launches; a split's plane words
+// become its partial sums as its stores land (an aligned 32-bit store is seen
+// whole or not at all).  The last split's workgroup loads the other splits'
+// words until none is EMPTY, folds them in ascending split order with its own
+// sums (in LDS, split S-1) last, finishes the output, then writes EMPTY back.
+// No partial sum can be the EMPTY pattern: FP16 operands make every NaN the
+// core produces carry 13 zero low bits, and EMPTY has none.  The poll is
+// bounded; a workgroup that gives up writes NaN outputs instead of hanging.
+constexpr uint32_t kPollLimit = 1u << 22;
+
+template <typename Plane>
+__device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeights& gw, const ColumnOperands& op,
+                                              float* y, int c, const float* own, Plane plane) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int others = int(a.splits) - 1;
+    for (uint32_t r = w; r < a.rows; r += GEMV_WAVES) {
+        float z0 = 0.0f, z1 = 0.0f;
+        bool complete = true;
+        for (int s = 0; s < others; s += kFoldBatch) {
+            float v0[kFoldBatch], v1[kFoldBatch];
+            for (uint32_t spin = 0;; ++spin) {
+                bool ready = true;
+#pragma unroll
+                for (int u = 0; u < kFoldBatch; ++u) {
+                    const float* p = plane(s + u < others ? s + u : others - 1, r);
+                    v0[u] = load_coherent(p + lane);
+                    v1[u] = load_coherent(p + lane + 64);
+                }
+#pragma unroll
+                for (int u = 0; u < kFoldBatch; ++u)
+                    ready = ready && (s + u >= others || (__builtin_bit_cast(uint32_t, v0[u]) != GEMV_PLANE_EMPTY &&
+                                                          __builtin_bit_cast(uint32_t, v1[u]) != GEMV_PLANE_EMPTY));
+                if (__all(ready)) break;
+                if (spin == kPollLimit) {
+                    complete = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+#pragma unroll
+            for (int u = 0; u < kFoldBatch; ++u) {
+                if (s + u < others) {
+                    z0 = z0 + v0[u];
+                    z1 = z1 + v1[u];
+                }
+            }
+        }
+        z0 = z0 + own[r * 128 + lane];
+        z1 = z1 + own[r * 128 + lane + 64];
+        if (!complete) z0 = z1 = __builtin_nanf("");
+        h32_wave(z0, z1);
+        const int n0 = 128 * c + lane, n1 = n0 + 64;
+        float* yr = y + r * a.y_row_stride;
+        const float o0 = output_value(z0, op.sv0, gw.bias != nullptr, op.b0, a.alpha, a.beta, yr + n0);
+        const float o1 = output_value(z1, op.sv1, gw.bias != nullptr, op.b1, a.alpha, a.beta, yr + n1);
+        *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+        *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+        const float empty = __builtin_bit_cast(float, GEMV_PLANE_EMPTY);
+        for (int s = 0; s < others; ++s) {
+            float* p = plane(s, r);
+            store_coherent(p + lane, empty);
+            store_coherent(p + lane + 64, empty);
+        }
+    }
+}
+
 // Dot of one decoded chunk (32 weights: columns g and g+8, rows 0..15 of one
 // input block) with the block's FP16 activations of every row.
 template <int RT>
@@ -155,7 +221,6 @@ __device__ __forceinline__ void dot_block(const half2_t (&wq)[4][4], const _Floa
 template <int K, int CB, int RT>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ int last_flag;
     const int c = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int jt = lane >> 3, g = lane & 7;
@@ -250,46 +315,30 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
+    // The single-launch finisher (mode 1) is the workgroup of the last split:
+    // it keeps its own sums in LDS; every other split publishes a plane.
+    const bool finisher = a.splits == 1 || (a.mode == 1 && uint32_t(s) == a.splits - 1);
     for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
         const int r = idx >> 7, n = idx & 127;
         float v = red[(0 * RT + r) * 128 + n];
 #pragma unroll
         for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + red[(ww * RT + r) * 128 + n];
-        if (a.splits == 1) {
+        if (finisher) {
             red[r * 128 + n] = v;
         } else if (uint32_t(r) < a.rows) {
             store_coherent(plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c + n, v);
         }
     }
+    if (!finisher) return;
+    const ColumnOperands op = column_operands(gw, c);
+    __syncthreads();
     if (a.splits == 1) {
-        const ColumnOperands op = column_operands(gw, c);
-        __syncthreads();
         finish_columns<false>(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
         return;
     }
-    if (a.mode == 0) return;
-
-    // Single-launch completion: the last workgroup of column group (z, c)
-    // finishes.  The coherent stores above are complete (waitcnt) before the
-    // counter increment; the finishing loads are issued after it returned.
-    // The finisher's svh/bias loads go out with the partial stores: the wait
-    // below covers both, so the finisher starts with its operands in registers.
-    const ColumnOperands op = column_operands(gw, c);
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    uint32_t* counter = a.counters + uint64_t(z) * (a.N >> 7) + c;
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = old == a.splits - 1;
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    finish_columns<true>(a, gw, op, y, c, a.splits, [&](int ss, int r) -> const float* {
+    finish_polled(a, gw, op, y, c, red, [&](int ss, int r) -> float* {
         return plane_base + (uint64_t(ss) * a.rows + r) * a.N + 128 * c;
     });
-    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Second launch of the two-kernel path: fold + output stage per column group.
