@@ -110,6 +110,23 @@ class TpMoeDeviceDesc(C.Structure):
                 ("reserved", u64 * 4)]
 
 
+class TpDensePairMember(C.Structure):
+    _fields_ = [("weights", vp), ("output", TensorDesc), ("alpha", f32), ("beta", f32)]
+
+
+class TpDensePairDesc(C.Structure):
+    _fields_ = [("struct_size", u32), ("abi_version", u32), ("input", TensorDesc),
+                ("member", TpDensePairMember * 2), ("workspace", vp), ("workspace_bytes", u64),
+                ("rows_per_block", u32), ("strategy", u32), ("reserved", u64 * 4)]
+
+
+class TpSwigluDesc(C.Structure):
+    _fields_ = [("struct_size", u32), ("abi_version", u32), ("input", TensorDesc), ("gate", vp), ("up", vp),
+                ("hidden_output", TensorDesc), ("workspace", vp), ("workspace_bytes", u64),
+                ("rows_per_block", u32), ("strategy", u32), ("diagnostic_gate", vp), ("diagnostic_up", vp),
+                ("diagnostic_bytes", u64), ("reserved", u64 * 4)]
+
+
 def header(struct_type, **fields):
     """Zero-initialised descriptor with struct_size / abi_version set."""
     d = struct_type()
@@ -165,6 +182,24 @@ _PROTOTYPES = {
     "strix_amd_gemv_shape": (_S, [vp, C.POINTER(u32), C.POINTER(u32)]),
     "strix_amd_plan_launches": (_S, [vp, C.POINTER(u32)]),
     "strix_amd_swiglu": (_S, [vp, vp, vp, vp, u64, C.POINTER(Stream)]),
+    "strix_tp_dense_plan_create": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), C.POINTER(vp)]),
+    "strix_tp_dense_plan_create_tiled": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), u32, C.POINTER(vp)]),
+    "strix_tp_dense_plan_create_splitk": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), u32, u32,
+                                               C.POINTER(vp)]),
+    "strix_tp_dense_plan_create_r1": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), u32, u32, C.POINTER(vp)]),
+    "strix_tp_dense_workspace_bytes": (_S, [vp, C.POINTER(MatmulDesc), u32, C.POINTER(u64)]),
+    "strix_tp_dense_plan_submit": (_S, [vp]),
+    "strix_tp_dense_plan_destroy": (_S, [vp]),
+    "strix_tp_dense_pair_desc_init": (None, [C.POINTER(TpDensePairDesc)]),
+    "strix_tp_swiglu_desc_init": (None, [C.POINTER(TpSwigluDesc)]),
+    "strix_tp_dense_pair_plan_create": (_S, [vp, C.POINTER(TpDensePairDesc), C.POINTER(Stream), C.POINTER(vp)]),
+    "strix_tp_dense_pair_plan_create_r1": (_S, [vp, C.POINTER(TpDensePairDesc), C.POINTER(Stream), u32,
+                                                C.POINTER(vp)]),
+    "strix_tp_dense_pair_plan_submit": (_S, [vp]),
+    "strix_tp_dense_pair_plan_destroy": (_S, [vp]),
+    "strix_tp_swiglu_plan_create": (_S, [vp, C.POINTER(TpSwigluDesc), C.POINTER(Stream), C.POINTER(vp)]),
+    "strix_tp_swiglu_plan_submit": (_S, [vp]),
+    "strix_tp_swiglu_plan_destroy": (_S, [vp]),
 }
 
 _lib = None

@@ -363,3 +363,107 @@ def swiglu(ctx, gate, up, stream=None):
                                        C.c_void_p(h.data_ptr()), gate.numel(), C.byref(stream_desc(stream))),
               "strix_amd_swiglu")
     return h
+
+
+def view_desc(t, rank=2):
+    """F32 descriptor of a row view: rank 2 [rows, width] with any row stride, or rank 1 [width]."""
+    if rank == 1:
+        return tensor_desc(t.reshape(-1), 1)
+    return row_view_desc(t)
+
+
+class TpDensePlan:
+    """Tensor-parallel dense projection on row views (strix_tp_dense_plan_*).
+
+    ``variant``: "plain", "tiled", "splitk" or "r1" (``param`` is rows_per_block;
+    ``strategy`` the split-K strategy or R1 identity)."""
+
+    def __init__(self, weights, x, y, alpha=1.0, beta=0.0, variant="plain", param=0, strategy=0, stream=None,
+                 rank=2):
+        self.lib = weights.lib
+        d = abi.MatmulDesc()
+        self.lib.strix_matmul_desc_init(C.byref(d))
+        d.weights = weights.handle
+        d.input = view_desc(x, rank)
+        d.output = view_desc(y, rank)
+        d.alpha, d.beta = alpha, beta
+        self._keep = (weights, x, y)
+        h = C.c_void_p()
+        sd = C.byref(stream_desc(stream))
+        if variant == "plain":
+            st = self.lib.strix_tp_dense_plan_create(weights.ctx.handle, C.byref(d), sd, C.byref(h))
+        elif variant == "tiled":
+            st = self.lib.strix_tp_dense_plan_create_tiled(weights.ctx.handle, C.byref(d), sd, param, C.byref(h))
+        elif variant == "splitk":
+            st = self.lib.strix_tp_dense_plan_create_splitk(weights.ctx.handle, C.byref(d), sd, param, strategy,
+                                                            C.byref(h))
+        else:
+            st = self.lib.strix_tp_dense_plan_create_r1(weights.ctx.handle, C.byref(d), sd, param, strategy,
+                                                        C.byref(h))
+        abi.check(st, "strix_tp_dense_plan_create")
+        self.handle = h
+
+    def submit(self):
+        abi.check(self.lib.strix_tp_dense_plan_submit(self.handle), "strix_tp_dense_plan_submit")
+
+    def destroy(self):
+        if self.handle:
+            abi.check(self.lib.strix_tp_dense_plan_destroy(self.handle), "strix_tp_dense_plan_destroy")
+            self.handle = None
+
+
+class TpPairPlan:
+    """Two projections of one input (q_a || kv): strix_tp_dense_pair_plan_*."""
+
+    def __init__(self, w0, w1, x, y0, y1, alphas=(1.0, 1.0), betas=(0.0, 0.0), stream=None):
+        self.lib = w0.lib
+        d = abi.TpDensePairDesc()
+        self.lib.strix_tp_dense_pair_desc_init(C.byref(d))
+        d.input = view_desc(x)
+        for i, (w, y) in enumerate(((w0, y0), (w1, y1))):
+            d.member[i].weights = w.handle
+            d.member[i].output = view_desc(y)
+            d.member[i].alpha = alphas[i]
+            d.member[i].beta = betas[i]
+        self._keep = (w0, w1, x, y0, y1)
+        h = C.c_void_p()
+        abi.check(self.lib.strix_tp_dense_pair_plan_create(w0.ctx.handle, C.byref(d), C.byref(stream_desc(stream)),
+                                                           C.byref(h)), "strix_tp_dense_pair_plan_create")
+        self.handle = h
+
+    def submit(self):
+        abi.check(self.lib.strix_tp_dense_pair_plan_submit(self.handle), "strix_tp_dense_pair_plan_submit")
+
+    def destroy(self):
+        if self.handle:
+            abi.check(self.lib.strix_tp_dense_pair_plan_destroy(self.handle), "strix_tp_dense_pair_plan_destroy")
+            self.handle = None
+
+
+class TpSwigluPlan:
+    """hidden = SwiGLU(gate(x), up(x)) (strix_tp_swiglu_plan_*); optional diagnostic gate/up outputs."""
+
+    def __init__(self, gate, up, x, hidden, diag_gate=None, diag_up=None, stream=None):
+        self.lib = gate.lib
+        d = abi.TpSwigluDesc()
+        self.lib.strix_tp_swiglu_desc_init(C.byref(d))
+        d.input = view_desc(x)
+        d.gate, d.up = gate.handle, up.handle
+        d.hidden_output = view_desc(hidden)
+        if diag_gate is not None:
+            d.diagnostic_gate = C.c_void_p(diag_gate.data_ptr())
+            d.diagnostic_up = C.c_void_p(diag_up.data_ptr())
+            d.diagnostic_bytes = diag_gate.numel() * 4
+        self._keep = (gate, up, x, hidden, diag_gate, diag_up)
+        h = C.c_void_p()
+        abi.check(self.lib.strix_tp_swiglu_plan_create(gate.ctx.handle, C.byref(d), C.byref(stream_desc(stream)),
+                                                       C.byref(h)), "strix_tp_swiglu_plan_create")
+        self.handle = h
+
+    def submit(self):
+        abi.check(self.lib.strix_tp_swiglu_plan_submit(self.handle), "strix_tp_swiglu_plan_submit")
+
+    def destroy(self):
+        if self.handle:
+            abi.check(self.lib.strix_tp_swiglu_plan_destroy(self.handle), "strix_tp_swiglu_plan_destroy")
+            self.handle = None

@@ -42,7 +42,8 @@ STRUCTS = {
     "strix_context_desc": abi.ContextDesc, "strix_tensor_desc": abi.TensorDesc, "strix_matmul_desc": abi.MatmulDesc,
     "strix_grouped_moe_desc": abi.GroupedMoeDesc, "strix_grouped_gemv_desc": abi.GroupedGemvDesc,
     "strix_tp_expert_desc": abi.TpExpertDesc, "strix_tp_moe_desc": abi.TpMoeDesc,
-    "strix_tp_moe_device_desc": abi.TpMoeDeviceDesc,
+    "strix_tp_moe_device_desc": abi.TpMoeDeviceDesc, "strix_tp_dense_pair_member": abi.TpDensePairMember,
+    "strix_tp_dense_pair_desc": abi.TpDensePairDesc, "strix_tp_swiglu_desc": abi.TpSwigluDesc,
 }
 
 
@@ -103,8 +104,13 @@ def test_context_header_validation_without_device():
     assert lib.strix_linear_plan_submit(None) == abi.STATUS_CODE["INVALID_ARGUMENT"]
 
 
-def test_tp_dense_entry_points_are_not_implemented():
+def test_tp_entry_points_validate_without_device():
     lib = abi.load()
     out = C.c_void_p(99)
-    assert lib.strix_tp_dense_plan_create(None, None, None, C.byref(out)) == abi.STATUS_CODE["NOT_IMPLEMENTED"]
+    # no context: rejected, output handle cleared
+    assert lib.strix_tp_dense_plan_create(None, None, None, C.byref(out)) == abi.STATUS_CODE["INVALID_ARGUMENT"]
+    assert out.value is None
+    # the integer-A8 MoE identity is not provided
+    out = C.c_void_p(99)
+    assert lib.strix_tp_moe_plan_create_a8r(None, None, None, C.byref(out)) == abi.STATUS_CODE["NOT_IMPLEMENTED"]
     assert out.value is None
