@@ -60,10 +60,37 @@ uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
     return align256(((r + 31) / 32) * 32 * w.input * 2);   // rows padded for either fragment order
 }
 
+// Column split of a wide pass over the 256 CUs (one 512-thread workgroup per
+// CU): `full` 256-column blocks run as 256 x 256 tiles, `half` as 256 x 128
+// tiles, twice the workgroups at half the work each.  A 256 x 128 tile takes
+// ~0.8 of a 256 x 256 tile's time (measured: the stage barrier and the A
+// stream do not shrink with it), so the narrow tiles are used only when all of
+// them fit one wave of workgroups and the wide ones would leave half the CUs
+// idle (M = 512 on 4096 -> 12288: 130 -> 115 us).
+struct WideSplit {
+    uint32_t full, half;   // 256-column blocks of each width
+};
+static WideSplit wide_split(uint64_t m, uint32_t n) {
+    constexpr uint64_t kCus = 256;
+    const uint64_t mb = (m + 255) / 256, nc = n / 256, tiles = mb * nc;
+    if (2 * tiles <= kCus) return {0, uint32_t(nc)};
+    return {uint32_t(nc), 0};
+}
+
+static bool gemm_wide(uint64_t m, const DeviceWeights& w) { return m >= 256 && w.output % 256 == 0; }
+
 uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows) {
-    if (!rows) return 0;
     const uint64_t pass = gemm_pass_rows(w);
-    return uint32_t(2 * ((rows + pass - 1) / pass));
+    uint32_t n = 0;
+    for (uint64_t r0 = 0; r0 < rows; r0 += pass) {
+        const uint64_t m = rows - r0 < pass ? rows - r0 : pass;
+        n += 2;
+        if (gemm_wide(m, w)) {
+            const WideSplit sp = wide_split(m, w.output);
+            n += sp.full && sp.half;
+        }
+    }
+    return n;
 }
 
 using GemmDispatch = hipError_t (*)(const GemmLaunch&);
@@ -89,7 +116,7 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         const uint64_t m = call.rows - r0 < pass ? call.rows - r0 : pass;
         // 256 x 256 tiles (32x16 fragments) once the rows fill them and N
         // splits into 256-column blocks; 128-row tiles (16x32 fragments) otherwise.
-        const bool wide = m >= 256 && w.output % 256 == 0;
+        const bool wide = gemm_wide(m, w);
         const uint32_t rb = wide ? 32 : 16;
         const uint64_t mpad = (m + rb - 1) / rb * rb;
         const float* x = call.x + r0 * call.x_row_stride;
@@ -116,8 +143,26 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         l.codebook = w.codebook;
         l.bm = gemm_bm(m, w.output / 128);
         l.stream = stream;
-        e = wide ? gemm_wide_table[w.bits - 1](l) : gemm_table[w.bits - 1](l);
-        if (e != hipSuccess) return e;
+        if (!wide) {
+            e = gemm_table[w.bits - 1](l);
+            if (e != hipSuccess) return e;
+            continue;
+        }
+        const WideSplit sp = wide_split(m, w.output);
+        if (sp.full) {
+            l.bn = 256;
+            l.col_blocks = sp.full;
+            l.args.col_block0 = 0;
+            e = gemm_wide_table[w.bits - 1](l);
+            if (e != hipSuccess) return e;
+        }
+        if (sp.half) {
+            l.bn = 128;
+            l.col_blocks = 2 * sp.half;
+            l.args.col_block0 = 2 * sp.full;
+            e = gemm_wide_table[w.bits - 1](l);
+            if (e != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }

@@ -41,6 +41,9 @@ struct GemmArgs {
     float* y;                 // [M][N]
     uint32_t M, I, N;
     float alpha, beta;
+    uint32_t col_block0;      // wide kernel: first column block of the launch,
+    uint32_t col_blocks;      // column blocks launched,
+    uint32_t tiles;           // and workgroups (column blocks x row blocks)
 };
 
 // Byte offset of the A fragment (row block rb, 32-channel block kb) of lane l.
@@ -210,6 +213,7 @@ struct GemmLaunch {
     GemmArgs args;
     uint32_t codebook;
     uint32_t bm;
+    uint32_t bn, col_blocks;  // wide kernel: tile width and column blocks launched
     hipStream_t stream;
 };
 

@@ -44,14 +44,27 @@ __host__ __device__ __forceinline__ uint64_t afrag32_offset(uint32_t rb, uint32_
     return ((uint64_t(rb) * (I / 16) + kb) * 64 + lane) * 16;
 }
 
-template <int K, int CB>
+// BN = 256: 8 waves as 2 (M) x 4 (N), each 128 x 64 (4 x 2 MFMA tiles), all
+// eight decode.  BN = 128: 4 (M) x 2 (N), each 64 x 64 (2 x 2 tiles); the
+// stage's B is 8 tiles x 4 blocks, decoded by waves 0..3 (one per SIMD) while
+// waves 4..7 issue empty chunk loads so every wave counts the same vmcnt.
+template <int K, int CB, int BN>
 __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
+    constexpr int WNW = BN / 64;                         // waves along N
+    constexpr int TI = 256 / (8 / WNW) / 32;             // 32-row MFMA tiles per wave
+    constexpr int TJ = 2;                                // 32-column MFMA tiles per wave
+    constexpr int NT = BN / 16;                          // trellis tiles per stage row
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char* abuf = smem;                          // 3 x [8 rb32][4 kb16][64][16 B]
-    unsigned char* bbuf = smem + 3 * WIDE_TILE_BYTES;    // 2 x [8 n32][4 kb16][64][16 B]
-    const int c = blockIdx.x, mb = blockIdx.y;           // c: 256-column block
+    unsigned char* bbuf = smem + 3 * WIDE_TILE_BYTES;    // 2 x [BN/32 n32][4 kb16][64][16 B]
+    // XCD-aware tile order: workgroup i runs on XCD i % 8 (round-robin
+    // dispatch), and each XCD takes a contiguous run of tiles in row-block-major
+    // order, so the workgroups of one XCD share A row blocks in its own L2.
+    uint32_t t = blockIdx.x;
+    if (a.tiles % 8 == 0) t = (t % 8) * (a.tiles / 8) + t / 8;
+    const int c = t % a.col_blocks + a.col_block0, mb = t / a.col_blocks;   // c: BN-column block
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int wm = w >> 2, wn = w & 3;
+    const int wm = w / WNW, wn = w % WNW;
     const int jt8 = lane >> 3, g = lane & 7;
     const uint32_t I = a.I, N = a.N, stages = I / 64;
 
@@ -59,14 +72,17 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     const uint32_t row_bytes = (N >> 4) * tile_bytes;
     const auto wrsrc = make_rsrc(a.trellis, uint32_t(uint64_t(I / 16) * row_bytes));
     const auto arsrc = make_rsrc(a.afrag, uint32_t(a.afrag_bytes));
-    const int dblk = w >> 1, dtile = 8 * (w & 1) + jt8;  // decode role
-    const uint32_t lane_off = (16u * c + dtile) * tile_bytes + g * 4u * K;
+    constexpr int kDecoders = NT * 4 / 8;                // wave units of 8 tiles x 1 block
+    const bool decoder = BN == 256 || w < kDecoders;
+    const int dblk = BN == 256 ? w >> 1 : w & 3;         // decode role
+    const int dtile = BN == 256 ? 8 * (w & 1) + jt8 : jt8;
+    const uint32_t lane_off = (uint32_t(NT) * c + dtile) * tile_bytes + g * 4u * K;
 
     // ---- B: chunk ring (stage st in slot st % D), one chunk per lane ----
     constexpr int D = 1;   // chunk ring depth; 2 would spill at 256 VGPRs
     Chunk<K> ring[D];
     auto load_stage = [&](Chunk<K>& dst, uint32_t st) {
-        load_chunk(dst, wrsrc, st < stages ? (st * 4 + dblk) * row_bytes + lane_off : 0x80000000u);
+        load_chunk(dst, wrsrc, (decoder && st < stages) ? (st * 4 + dblk) * row_bytes + lane_off : 0x80000000u);
     };
     // Lane (tile dtile, chunk g) holds rows 0..15 of tile columns g and g+8 of
     // input block dblk: column n = 16 (dtile % 2) + g (+8) of 32-column block
@@ -81,6 +97,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         *frag(40 + n) = u32x4{as_u32(wq[0][3]), as_u32(wq[1][3]), as_u32(wq[2][3]), as_u32(wq[3][3])};
     };
     auto decode_stage = [&](Chunk<K>& src, int buf) {
+        if (!decoder) return;
         link_chunk(src, g == 0);
         half2_t wq[4][4];
         decode_chunk<K, CB>(src, wq);
@@ -117,11 +134,11 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(v) : "memory");
     };
 
-    float16_t acc[4][2];
+    float16_t acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = float16_t{};
+        for (int j = 0; j < TJ; ++j) acc[i][j] = float16_t{};
 
     // Prologue: A stages 0 and 1 in flight, B stage 0 decoded, chunk ring full.
 #pragma unroll
@@ -151,28 +168,37 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             const unsigned char* bb = bbuf + (st & 1) * WIDE_TILE_BYTES;
             const int slot = (d + 1) % D;   // compile-time after unrolling
             Chunk<K>& dc = ring[slot];
-            link_chunk(dc, g == 0);
+            if (decoder) link_chunk(dc, g == 0);
             half2_t wq[4][4];
+            // Fragments of K16 step kb + 1 are read while step kb multiplies.
+            half8_t bf[2][TJ], af[2][TI];
+            auto read_frags = [&](int kb) {
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    bf[kb & 1][j] = *reinterpret_cast<const half8_t*>(bb + (((TJ * wn + j) * 4 + kb) * 64 + lane) * 16);
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+                    af[kb & 1][i] = *reinterpret_cast<const half8_t*>(ab + (((TI * wm + i) * 4 + kb) * 64 + lane) * 16);
+            };
+            read_frags(0);
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-                half8_t bf[2], af[4];
+                if (kb < 3) read_frags(kb + 1);
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    bf[j] = *reinterpret_cast<const half8_t*>(bb + (((2 * wn + j) * 4 + kb) * 64 + lane) * 16);
+                for (int i = 0; i < TI; ++i) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    af[i] = *reinterpret_cast<const half8_t*>(ab + (((4 * wm + i) * 4 + kb) * 64 + lane) * 16);
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kb & 1][i], bf[kb & 1][j], acc[i][j], 0, 0, 0);
+                    // 16 weight pairs per stage, spread over the TI x 4 MFMA groups
+                    if (decoder) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-                    decode_pair_at<K, CB>(dc, wq, 4 * kb + i);
+                        for (int q = 0; q < 4 / TI; ++q) decode_pair_at<K, CB>(dc, wq, 4 * kb + (4 / TI) * i + q);
+                    }
                 }
             }
             // Decoded stage st + 1 -> the other B buffer (past the end: zeros
             // of out-of-range loads into an unused buffer).
-            store_bfrag(wq, (st + 1) & 1);
+            if (decoder) store_bfrag(wq, (st + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
             load_stage(ring[slot], st + 1 + D);
             __builtin_amdgcn_sched_barrier(0);
@@ -182,42 +208,52 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         }
     }
 
-    // ---- Epilogue: rows [128 p, +128) through an LDS [128][256] FP32 tile ----
-    // A wave always finishes column group w % 2 of its rows, so its svh and
-    // bias operands are loaded once, ahead of the first pass.
-    const int grp = w & 1;
-    const uint32_t n0 = 256u * c + 128u * grp + lane, n1 = n0 + 64;
+    // ---- Epilogue: rows [128 p, +128) through an LDS [128][BN] FP32 tile ----
+    // A wave always finishes column group w % (BN/128) of its rows, so its svh
+    // and bias operands are loaded once, ahead of the first pass.
+    constexpr int GROUPS = BN / 128;
+    const int grp = w % GROUPS;
+    const uint32_t n0 = uint32_t(BN) * c + 128u * grp + lane, n1 = n0 + 64;
     const uint16_t sv0 = ld_global(a.svh + n0), sv1 = ld_global(a.svh + n1);
     const bool has_bias = a.bias != nullptr;
     const float b0 = has_bias ? ld_global(a.bias + n0) : 0.0f, b1 = has_bias ? ld_global(a.bias + n1) : 0.0f;
     float* tile = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-        if (wm == p) {
+        if ((32 * TI * wm) / 128 == p) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TJ; ++j)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int row = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        const int row = (32 * TI * wm) % 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                         const int col = 64 * wn + 32 * j + (lane & 31);
                         tile[row * WIDE_EPI_STRIDE + col] = acc[i][j][r];
                     }
         }
         __syncthreads();
-        // 128 rows x 2 column groups; wave w takes rows w/2, w/2 + 4, ... of group w % 2.
-        for (int rr = w >> 1; rr < 128; rr += 4) {
-            const uint32_t row = uint32_t(mb) * 256 + 128 * p + rr;
-            float z0 = tile[rr * WIDE_EPI_STRIDE + 128 * grp + lane];
-            float z1 = tile[rr * WIDE_EPI_STRIDE + 128 * grp + lane + 64];
-            h32_wave(z0, z1);
-            if (row < a.M) {
-                float* yr = a.y + uint64_t(row) * N;
-                const float o0 = output_value(z0, sv0, has_bias, b0, a.alpha, a.beta, yr + n0);
-                const float o1 = output_value(z1, sv1, has_bias, b1, a.alpha, a.beta, yr + n1);
-                *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
-                *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+        // 128 rows x GROUPS column groups; wave w takes rows w/GROUPS + RS q of
+        // group w % GROUPS, four rows per step with their butterflies interleaved.
+        constexpr int RS = 8 / GROUPS;
+        for (int r0 = w / GROUPS; r0 < 128; r0 += 4 * RS) {
+            float z0[4], z1[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                z0[q] = tile[(r0 + RS * q) * WIDE_EPI_STRIDE + 128 * grp + lane];
+                z1[q] = tile[(r0 + RS * q) * WIDE_EPI_STRIDE + 128 * grp + lane + 64];
+            }
+            h32_wave_multi<4>(z0, z1);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t row = uint32_t(mb) * 256 + 128 * p + r0 + RS * q;
+                if (row < a.M) {
+                    float* yr = a.y + uint64_t(row) * N;
+                    const float o0 = output_value(z0[q], sv0, has_bias, b0, a.alpha, a.beta, yr + n0);
+                    const float o1 = output_value(z1[q], sv1, has_bias, b1, a.alpha, a.beta, yr + n1);
+                    *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+                    *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+                }
             }
         }
         __syncthreads();
@@ -231,18 +267,24 @@ hipError_t gemm_wide_dispatch(const GemmLaunch& l);
     template <>                                                                                        \
     hipError_t gemm_wide_dispatch<K>(const GemmLaunch& l) {                                            \
         using Fn = void (*)(GemmArgs);                                                                 \
-        static const Fn table[3] = {gemm_wide_kernel<K, 0>, gemm_wide_kernel<K, 1>, gemm_wide_kernel<K, 2>}; \
+        static const Fn table[2][3] = {                                                                \
+            {gemm_wide_kernel<K, 0, 256>, gemm_wide_kernel<K, 1, 256>, gemm_wide_kernel<K, 2, 256>},   \
+            {gemm_wide_kernel<K, 0, 128>, gemm_wide_kernel<K, 1, 128>, gemm_wide_kernel<K, 2, 128>}};  \
         static const hipError_t attr = [] {                                                            \
-            for (Fn f : table) {                                                                       \
-                const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(f),             \
-                    hipFuncAttributeMaxDynamicSharedMemorySize, int(WIDE_LDS_BYTES));                   \
-                if (e != hipSuccess) return e;                                                         \
-            }                                                                                          \
+            for (const auto& row : table)                                                              \
+                for (Fn f : row) {                                                                     \
+                    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(f),         \
+                        hipFuncAttributeMaxDynamicSharedMemorySize, int(WIDE_LDS_BYTES));               \
+                    if (e != hipSuccess) return e;                                                     \
+                }                                                                                      \
             return hipSuccess;                                                                         \
         }();                                                                                           \
         if (attr != hipSuccess) return attr;                                                           \
-        const dim3 grid(l.args.N / 256, (l.args.M + 255) / 256);                                       \
-        hipLaunchKernelGGL(table[l.codebook], grid, dim3(512), WIDE_LDS_BYTES, l.stream, l.args);  \
+        if (l.bn != 256 && l.bn != 128) return hipErrorInvalidValue;                                   \
+        GemmArgs args = l.args;                                                                        \
+        args.col_blocks = l.col_blocks;                                                                \
+        args.tiles = l.col_blocks * ((l.args.M + 255) / 256);                                          \
+        hipLaunchKernelGGL(table[l.bn == 128][l.codebook], dim3(args.tiles), dim3(512), WIDE_LDS_BYTES, l.stream, args); \
         return hipGetLastError();                                                                      \
     }
 

@@ -11,6 +11,8 @@
 // holds elements l and l+64; strides 1..32 pair lanes through shuffles, stride
 // 64 pairs the two registers of a lane.
 #pragma once
+#include <type_traits>
+
 #include "trellis.hpp"
 
 namespace stx {
@@ -68,6 +70,39 @@ __device__ __forceinline__ void h32_wave(float& v0, float& v1) {
     v1 = rn32(a - b);
     v0 = rn32(v0 * INV_SQRT128);
     v1 = rn32(v1 * INV_SQRT128);
+}
+
+// H32 of P independent (v0, v1) pairs, stage by stage across the pairs so
+// their dependency chains interleave (same operations, same bits as h32_wave).
+template <int P>
+__device__ __forceinline__ void h32_wave_multi(float (&v0)[P], float (&v1)[P]) {
+    auto stage = [&](auto s) {
+        constexpr int S = decltype(s)::value;
+        const bool upper = (threadIdx.x & S) != 0;
+        float p0[P], p1[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            p0[i] = xor_lane<S>(v0[i]);
+            p1[i] = xor_lane<S>(v1[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            v0[i] = upper ? p0[i] - v0[i] : v0[i] + p0[i];
+            v1[i] = upper ? p1[i] - v1[i] : v1[i] + p1[i];
+        }
+    };
+    stage(std::integral_constant<int, 1>{});
+    stage(std::integral_constant<int, 2>{});
+    stage(std::integral_constant<int, 4>{});
+    stage(std::integral_constant<int, 8>{});
+    stage(std::integral_constant<int, 16>{});
+    stage(std::integral_constant<int, 32>{});
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const float a = v0[i], b = v1[i];
+        v0[i] = rn32(rn32(a + b) * INV_SQRT128);
+        v1[i] = rn32(rn32(a - b) * INV_SQRT128);
+    }
 }
 
 // Input stage of one 128-block, split into the loads and the arithmetic so a

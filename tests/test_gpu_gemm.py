@@ -102,3 +102,28 @@ def test_gemm_rows_independent_of_batch_and_alpha_beta(ctx):
         assert torch.equal(yp.view(torch.int32), y_all.view(torch.int32))
     plan.destroy()
     w.destroy()
+
+
+@pytest.mark.parametrize("N", [8448, 8192])
+def test_gemm_tile_widths_agree(ctx, N):
+    # M = 2048 over N = 8448 runs 32 column blocks as 256 x 256 tiles and the
+    # last as 256 x 128 tiles; N = 8192 fills the 256 CUs with 256 x 256 tiles
+    # only.  256 rows run as 256 x 128 tiles, 16 rows on the 128-row kernel:
+    # every row has the same bits whichever tile computes it.
+    I, K, M = 256, 4, 2048
+    print(f"gemm tile widths M={M} {I}x{N} K={K}", flush=True)
+    tr, suh, svh, b = synth.layer(I, N, K, 90 + N, bias=True)
+    w = runtime.Weights(ctx, tr, suh, svh, b, "mul1")
+    x = torch.from_numpy(synth.activations(M, I, 93)).to(DEV)
+    y = torch.full((M, N), float("nan"), device=DEV)
+    runtime.gemm(w, x, y)
+    for rows in (256, 16):
+        yr = torch.full((rows, N), float("nan"), device=DEV)
+        runtime.gemm(w, x[M - rows:].contiguous(), yr)
+        assert torch.equal(yr.view(torch.int32), y[M - rows:].view(torch.int32)), rows
+    torch.cuda.synchronize()
+    sel = np.r_[0:24, 1000:1016, M - 24:M]
+    q = codec.dequantize_rotated(tr, K, "mul1")
+    ref = linear.matmul_fp32_stages(x.cpu().numpy()[sel], tr, suh, svh, K, "mul1", b, rotated=q)["output_fp32"]
+    synth.gate(y.cpu().numpy()[sel], ref)
+    w.destroy()
