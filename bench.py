@@ -11,6 +11,10 @@ Also reported on the same JSON line:
   grouped_o_a    16 groups x (4096 -> 1024) K5, R = 1..8, one grouped plan
   moe_k2         64 experts (4096 <-> 1536, K2), 8 tokens, top-8, device routes
   roofline       the headline kernel: packed bytes / its mean launch time
+  fp16_library   per GEMV/GEMM cell: the same product on dense FP16 weights
+                 through torch.matmul (hipBLASLt / rocBLAS), random-normal
+                 operands, same rotation and timing -- the vendor library's
+                 speed on the unquantised layer, for comparison
   cpu_baseline   the NumPy oracle on the host cores, bounded sample
 
 Timing: each rotation pass (one launch per weight copy) is captured once into
@@ -128,6 +132,51 @@ def time_rotation(rot, steps, warmup):
             "timed_steps": passes * rot.copies, "passes": passes, "output_check": ok_before and ok_after}
 
 
+_LIBRARY = {}
+
+
+def library_fp16(M, I, N, passes=5):
+    """The same product, y[M][N] = x[M][I] @ W[I][N], on dense FP16 weights
+    through torch.matmul (hipBLASLt / rocBLAS), random-normal operands: weight
+    copies rotated over >= ROTATION_BYTES, one pass captured in a HIP graph,
+    median pass time over HIP events.  Cached per shape."""
+    import torch
+    key = (M, I, N)
+    if key in _LIBRARY:
+        return _LIBRARY[key]
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(M * 131 + I * 7 + N)
+    copies = max(2, -(-ROTATION_BYTES // (2 * I * N)))
+    ws = [torch.randn((I, N), device=dev, dtype=torch.float16, generator=g) for _ in range(copies)]
+    x = torch.randn((M, I), device=dev, dtype=torch.float16, generator=g)
+    ys = [torch.empty((M, N), device=dev, dtype=torch.float16) for _ in range(2)]
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(copies):
+            torch.matmul(x, ws[i], out=ys[i & 1])
+    torch.cuda.synchronize()
+    expected = [ys[(copies - 2) & 1].clone(), ys[(copies - 1) & 1].clone()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(copies):
+            torch.matmul(x, ws[i], out=ys[i & 1])
+    graph.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(passes + 1)]
+    with torch.cuda.stream(stream):
+        ev[0].record(stream)
+        for i in range(passes):
+            graph.replay()
+            ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.median(ev[i].elapsed_time(ev[i + 1]) / copies for i in range(passes))
+    same = all(torch.equal(ys[(copies - 2 + j) & 1], expected[j]) for j in range(2)) if copies >= 2 else True
+    del graph, ws
+    out = {"us": round(ms * 1e3, 3), "replay_matches_eager": bool(same)}
+    _LIBRARY[key] = out
+    return out
+
+
 def bench_gemv(ctx, I, N, K, R, steps, warmup, seed):
     rot = Rotation(ctx, I, N, K, R, seed, "gemv")
     try:
@@ -135,9 +184,11 @@ def bench_gemv(ctx, I, N, K, R, steps, warmup, seed):
     finally:
         rot.close()
     gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
+    lib = library_fp16(R, I, N)
     return {"I": I, "N": N, "K": K, "R": R, "us": round(t["ms"] * 1e3, 3), "packed_GBps": round(gbps, 1),
             "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "launches": rot.launches,
-            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"],
+            "fp16_library_us": lib["us"], "speedup_vs_fp16_library": round(lib["us"] / (t["ms"] * 1e3), 2)}
 
 
 def bench_gemm(ctx, M, I, N, K, steps, warmup, seed):
@@ -147,9 +198,13 @@ def bench_gemm(ctx, M, I, N, K, steps, warmup, seed):
     finally:
         rot.close()
     tflops = 2.0 * M * I * N / (t["ms"] * 1e-3) / 1e12
+    lib = library_fp16(M, I, N)
+    lib_tflops = 2.0 * M * I * N / (lib["us"] * 1e-6) / 1e12
     return {"M": M, "I": I, "N": N, "K": K, "us": round(t["ms"] * 1e3, 2), "TFLOPs": round(tflops, 1),
             "pct_fp16_peak": round(100 * tflops / FP16_PEAK_TFLOPS, 1), "launches": rot.launches,
-            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"],
+            "fp16_library_us": lib["us"], "fp16_library_pct_peak": round(100 * lib_tflops / FP16_PEAK_TFLOPS, 1),
+            "speedup_vs_fp16_library": round(lib["us"] / (t["ms"] * 1e3), 2)}
 
 
 def bench_grouped(ctx, G, I, N, K, R, steps, warmup, seed):
@@ -406,7 +461,8 @@ def main():
         "config": {"workload": "decode GEMV R1, EXL3 K4 mul1, I=N=4096, prepared single-launch plan, "
                                f"cold rotation over {head['rotation_copies']} weight copies (>=1 GiB)",
                    "us_per_call": head["us"], "pct_hbm_peak": head["pct_hbm_peak"],
-                   "bit_identical": head["bit_identical"]},
+                   "bit_identical": head["bit_identical"], "fp16_library_us": head["fp16_library_us"],
+                   "speedup_vs_fp16_library": head["speedup_vs_fp16_library"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _traffic(),
                      "kernel": HEADLINE_KERNEL, "algorithmic_bytes_per_launch": 4096 * 4096 * 4 // 8,
@@ -418,11 +474,13 @@ def main():
         "moe_k2": moe_cell,
     }
     if gemm:
-        best = {}
+        best, lib = {}, {}
         for c in gemm:
             if c["M"] == 2048:
                 best[f"{c['I']}x{c['N']} K{c['K']}"] = c["pct_fp16_peak"]
+                lib[f"{c['I']}x{c['N']}"] = c["fp16_library_pct_peak"]
         out["prefill_m2048_pct_fp16_peak"] = best
+        out["prefill_m2048_fp16_library_pct_peak"] = lib
     print(json.dumps(out), flush=True)
 
 
