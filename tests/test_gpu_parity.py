@@ -232,6 +232,32 @@ def test_grouped_gemv_equals_individual(ctx):
         w.destroy()
 
 
+@pytest.mark.parametrize("I,N,K,G,R", [(2048, 1024, 5, 16, 1), (4096, 1024, 5, 16, 1), (4096, 1024, 5, 16, 2),
+                                       (4096, 1024, 4, 16, 5)])
+def test_grouped_large_grids_equal_individual(ctx, I, N, K, G, R):
+    # Grouped plans at the benchmark shape (16 x 4096 -> 1024: 4096 workgroups
+    # at R = 1, several rounds of resident workgroups): each group's rows stay
+    # bit-identical to strix_gemv on that layer alone.
+    print(f"grouped large grid {G}x {I}x{N} K={K} R={R}", flush=True)
+    ws = [_weights(ctx, I, N, K, 700 + g, bias=(g % 3 == 0))[0] for g in range(G)]
+    x = torch.from_numpy(synth.activations(R, G * I, 13)).to(DEV)
+    y = torch.empty((R, G * N), device=DEV)
+    plan = runtime.GroupedGemvPlan(ws, x, y, R, igs=I, ogs=N, irs=G * I, ors=G * N)
+    ref = torch.empty((R, G * N), device=DEV)
+    for g in range(G):
+        yg = torch.empty((R, N), device=DEV)
+        runtime.gemv(ws[g], x[:, g * I:(g + 1) * I].contiguous(), yg)
+        ref[:, g * N:(g + 1) * N] = yg
+    for _ in range(3):
+        y.fill_(float("nan"))
+        plan.submit()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+    plan.destroy()
+    for w in ws:
+        w.destroy()
+
+
 def test_errors_and_empty_rows(ctx):
     lib = ctx.lib
     w, _ = _weights(ctx, 256, 128, 4, 1)
