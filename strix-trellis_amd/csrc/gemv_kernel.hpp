@@ -9,8 +9,8 @@
 //   (16 channels each, bps a multiple of 8 so the split holds whole H128
 //   input blocks).
 //   * prologue: the workgroup computes the FP16 core input of its channels
-//     into LDS (one wave per 128-block); the first weight loads are issued
-//     before it so their latency overlaps it;
+//     into LDS (one wave per 128-block); the weight loads of the prefetch
+//     ring are issued before it so their latency overlaps it;
 //   * main loop: wave w takes input blocks w, w+4, ...; per block every lane
 //     loads its K-word chunk (K*256 contiguous bytes per wave), decodes 32
 //     weights in VGPRs and runs, per row, two v_dot2 chains (columns g, g+8)
@@ -218,8 +218,16 @@ __device__ __forceinline__ void dot_block(const half2_t (&wq)[4][4], const _Floa
     }
 }
 
+// Register budget: five waves per SIMD (<= 96 VGPRs), measured faster than
+// four (C1 8.9 -> 8.3 us; 16 x 4096 -> 1024 R4 32.5 -> 30.4 us) even where the
+// grid is smaller than one resident round.  The 8-row K >= 6 instances would
+// spill at that budget and keep four.
+template <int K, int RT>
+constexpr int gemv_waves_per_eu() { return RT == 8 && K >= 6 ? 4 : 5; }
+
 template <int K, int CB, int RT>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu<K, RT>())))
+void gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int c = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -272,31 +280,23 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     // this VALU work overlaps the latency of the input-stage loads (which
     // queue behind the weight traffic of the whole grid) and of the other
     // waves' H128 shuffles.  Their slots are refilled with blocks 4 and 5.
-    const bool first = g == 0;
-    half2_t d0[4][4], d1[4][4];
-    link_chunk(ring[0], first);
-    decode_chunk<K, CB>(ring[0], d0);
-    load_chunk(ring[0], rsrc, block_off(4));
-    link_chunk(ring[1], first);
-    decode_chunk<K, CB>(ring[1], d1);   // nb >= 2 always
-    load_chunk(ring[1], rsrc, block_off(5));
-
+    // The chunks stay in their registers across the input stage: decoding
+    // blocks ahead of the barrier (to overlap the input loads) was measured
+    // slower, the decoded weights holding 32 more VGPRs per lane.
     if (w < units) input_compute(pre0, unit_out(w));
     if (w + GEMV_WAVES < units) input_compute(pre1, unit_out(w + GEMV_WAVES));
     for (int u = w + 2 * GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
     __syncthreads();
 
+    const bool first = g == 0;
     float acc[RT][2];
 #pragma unroll
     for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
-    dot_block<RT>(d0, act + w * 16, act_row, acc);
-    dot_block<RT>(d1, act + (w + GEMV_WAVES) * 16, act_row, acc);
-
-    // Blocks t >= 2: slot (t + 2) % 4 holds block t; it is refilled with block t + 4.
-    for (int t = 2; t < nb; t += 4) {
+    // Slot t % 4 holds block t; it is refilled with block t + 4.
+    for (int t = 0; t < nb; t += 4) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            Chunk<K>& slot = ring[(u + 2) & 3];
+            Chunk<K>& slot = ring[u];
             if (t + u < nb) {
                 half2_t wq[4][4];
                 link_chunk(slot, first);
