@@ -116,7 +116,7 @@ strix_status common_check(strix_context c, const D* d, uint64_t routes_per_row, 
                      {e.up->dev.trellis, e.up->dev.suh, e.up->dev.svh, e.up->dev.bias},
                      {e.down->dev.trellis, e.down->dev.suh, e.down->dev.svh, e.down->dev.bias}};
     }
-    const stx::MoeSplit sgu = stx::moe_split(I), sd = stx::moe_split(H);
+    const stx::MoeSplit sgu = stx::moe_split(I, stx::MOE_GU_MAX_BPS), sd = stx::moe_split(H, stx::MOE_D_MAX_BPS);
     stx::MoeArgs& a = v.args;
     a.rows = uint32_t(rows);
     a.topk = uint32_t(routes_per_row);

@@ -3,16 +3,17 @@
 
 namespace stx {
 
-MoeSplit moe_split(uint32_t input) {
+MoeSplit moe_split(uint32_t input, uint32_t max_bps) {
     const uint32_t blocks = input / 16;
     uint32_t bps = 8;
-    for (uint32_t b = 16; b <= uint32_t(MOE_MAX_BPS); b += 8)
+    for (uint32_t b = 16; b <= max_bps; b += 8)
         if (blocks % b == 0) bps = b;
     return {bps, blocks / bps};
 }
 
 uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H) {
-    return uint64_t(routes) * moe_split(I).splits * 2 * H + uint64_t(routes) * moe_split(H).splits * I;
+    return uint64_t(routes) * moe_split(I, MOE_GU_MAX_BPS).splits * 2 * H +
+           uint64_t(routes) * moe_split(H, MOE_D_MAX_BPS).splits * I;
 }
 
 uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H) {
@@ -27,8 +28,8 @@ static bool moe_args_ok(const MoeArgs& a) {
     const uint32_t routes = a.rows * a.topk;
     return a.rows >= 1 && a.rows <= 8 && a.topk >= 1 && a.topk <= MOE_MAX_TOPK && routes <= MOE_MAX_ROUTES &&
            a.I % 128 == 0 && a.H % 128 == 0 && a.gate_bits >= 2 && a.gate_bits <= 3 && a.up_bits >= 2 &&
-           a.up_bits <= 3 && a.down_bits >= 2 && a.down_bits <= 3 && a.bps_gu <= uint32_t(MOE_MAX_BPS) &&
-           a.bps_d <= uint32_t(MOE_MAX_BPS) && a.bps_gu % 8 == 0 && a.bps_d % 8 == 0 &&
+           a.up_bits <= 3 && a.down_bits >= 2 && a.down_bits <= 3 && a.bps_gu <= uint32_t(MOE_GU_MAX_BPS) &&
+           a.bps_d <= uint32_t(MOE_D_MAX_BPS) && a.bps_gu % 8 == 0 && a.bps_d % 8 == 0 &&
            a.bps_gu * a.s_gu * 16 == a.I && a.bps_d * a.s_d * 16 == a.H;
 }
 

@@ -46,11 +46,15 @@ struct MoeArgs {
 };
 
 // Split-K decomposition of one MoE projection with `blocks` 16-channel input
-// blocks: the largest whole-H128 split of at most 32 blocks.
+// blocks: the largest whole-H128 split of at most max_bps blocks.  Long splits
+// amortise each workgroup's route resolution and input stage over more decode
+// work; the maxima size the kernels' LDS activation buffers.
 struct MoeSplit {
     uint32_t bps, splits;
 };
-MoeSplit moe_split(uint32_t input);
+constexpr int MOE_GU_MAX_BPS = 64;   // gate/up: input I
+constexpr int MOE_D_MAX_BPS = 96;    // down: input H
+MoeSplit moe_split(uint32_t input, uint32_t max_bps);
 uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
 uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H);
 

@@ -150,7 +150,6 @@ __device__ __forceinline__ void moe_release() {
     __syncthreads();
 }
 
-constexpr int MOE_MAX_BPS = 32;
 constexpr int MOE_MAX_RT = 8;
 // Chunk loads in flight per wave and projection.  K2/K3 chunks are 8-12 bytes
 // per lane, so deep rings are what keeps enough bytes in flight per CU.
@@ -158,9 +157,9 @@ constexpr int MOE_RING_GU = 4;
 constexpr int MOE_RING_D = 8;
 // LDS: the FP16 activations live until the main loop ends, the wave partials
 // only after it, so both share one buffer.
-constexpr int MOE_GU_ACT_BYTES = 2 * MOE_MAX_RT * MOE_MAX_BPS * 16 * 2;
+constexpr int MOE_GU_ACT_BYTES = 2 * MOE_MAX_RT * MOE_GU_MAX_BPS * 16 * 2;
 constexpr int MOE_GU_RED_BYTES = GEMV_WAVES * 2 * MOE_MAX_RT * 128 * 4;
-constexpr int MOE_D_ACT_BYTES = MOE_MAX_RT * MOE_MAX_BPS * 16 * 2;
+constexpr int MOE_D_ACT_BYTES = MOE_MAX_RT * MOE_D_MAX_BPS * 16 * 2;
 constexpr int MOE_D_RED_BYTES = GEMV_WAVES * MOE_MAX_RT * 128 * 4;
 constexpr int moe_max(int a, int b) { return a > b ? a : b; }
 
