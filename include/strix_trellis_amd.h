@@ -48,6 +48,15 @@ strix_status strix_amd_plan_launches(strix_linear_plan plan, uint32_t *launches)
 strix_status strix_amd_swiglu(strix_context context, const float *gate, const float *up, float *hidden,
     uint64_t count, const strix_stream *stream);
 
+/* Test hook for the prefill GEMM's split-tile handoff (M = 2048-class passes
+ * whose 256 x 256 tile count exceeds a multiple of 256 by at most 128).  The
+ * second workgroup of a split tile normally continues from the first one's
+ * published FP32 accumulators and only recomputes the first half of K itself
+ * when that publication is late (bounded wait).  always_take_over != 0 makes
+ * every later call and plan created on this context take that recompute path;
+ * 0 restores the default.  Outputs are bit-identical either way. */
+strix_status strix_amd_set_gemm_handoff(strix_context context, uint32_t always_take_over);
+
 #ifdef __cplusplus
 }
 #endif

@@ -313,6 +313,7 @@ stx::LinearCall make_call(const strix_matmul_desc& d, uint64_t rows, void* works
     lc.alpha = d.alpha;
     lc.beta = d.beta;
     lc.workspace = workspace;
+    lc.handoff_poll_limit = d.weights->owner->gemm_handoff_poll;
     return lc;
 }
 
@@ -689,6 +690,13 @@ strix_status strix_amd_plan_launches(strix_linear_plan p, uint32_t* launches) {
     if (launches) *launches = 0;
     if (!p || !launches) return STRIX_ERROR_INVALID_ARGUMENT;
     *launches = p->launches;
+    return STRIX_SUCCESS;
+}
+
+strix_status strix_amd_set_gemm_handoff(strix_context c, uint32_t always_take_over) {
+    const strix_status s = context_ok(c);
+    if (s != STRIX_SUCCESS) return s;
+    c->gemm_handoff_poll = always_take_over ? UINT32_MAX : 4096u;
     return STRIX_SUCCESS;
 }
 

@@ -11,6 +11,7 @@ struct strix_context_impl {
     int device = -1;
     int compute_units = 0;
     uint64_t weights_live = 0;
+    uint32_t gemm_handoff_poll = 4096;   // LinearCall::handoff_poll_limit of calls made on it
 };
 
 struct strix_weights_impl {

@@ -56,6 +56,9 @@ struct LinearCall {
     float alpha = 1.0f;
     float beta = 0.0f;
     void* workspace = nullptr;
+    // Prefill GEMM split-tile handoff: polls before the second workgroup of a
+    // split tile takes it over from K = 0 (UINT32_MAX: always, a test hook).
+    uint32_t handoff_poll_limit = 4096;
 };
 
 // Generic GEMV (rows 1..8): core kernel + finishing kernel, no counters.

@@ -9,12 +9,16 @@ namespace stx {
 // LDS tile; then every thread writes whole fragment lanes -- 8 consecutive
 // channels of one row, 16 contiguous bytes -- so each fragment (64 lanes x
 // 16 B) is one coalesced 1 KiB store.  Rows past M are zero.
+// Workgroup (0, 0) also clears the wide GEMM's `nflags` handoff flags.
 template <int RB>
 __global__ __launch_bounds__(256) void input_stage_frag_kernel(const float* x, const uint16_t* suh, uint32_t M,
-                                                               uint32_t I, _Float16* afrag) {
+                                                               uint32_t I, _Float16* afrag, uint32_t* flags,
+                                                               uint32_t nflags) {
     __shared__ __align__(16) _Float16 tile[RB][128 + 8];
     const uint32_t blk = blockIdx.x, rb = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    if (blk == 0 && rb == 0)
+        for (uint32_t i = tid; i < nflags; i += 256) flags[i] = 0;
     const uint32_t ch = blk * 128;
 #pragma unroll
     for (int q = 0; q < RB / 4; ++q) {
@@ -54,10 +58,8 @@ static uint64_t gemm_pass_rows(const DeviceWeights& w) {
 
 static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
 
-uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
-    const uint64_t pass = gemm_pass_rows(w);
-    const uint64_t r = rows < pass ? rows : pass;
-    return align256(((r + 31) / 32) * 32 * w.input * 2);   // rows padded for either fragment order
+static uint64_t afrag_bytes(const DeviceWeights& w, uint64_t m) {
+    return align256(((m + 31) / 32) * 32 * w.input * 2);   // rows padded for either fragment order
 }
 
 // Column split of a wide pass over the 256 CUs (one 512-thread workgroup per
@@ -78,6 +80,40 @@ static WideSplit wide_split(uint64_t m, uint32_t n) {
 }
 
 static bool gemm_wide(uint64_t m, const DeviceWeights& w) { return m >= 256 && w.output % 256 == 0; }
+
+// K-split handoff of a wide pass with only 256 x 256 tiles: T = 256 q + x
+// tiles with 0 < x <= 128 (and T a multiple of the 8 XCDs) launch as x
+// heads, 256 q whole tiles and x tails (one workgroup per CU at a time), so
+// each CU runs about q + 1/2 tile-times instead of q + 1.
+struct Handoff {
+    uint32_t q = 0, x = 0;
+};
+static Handoff gemm_handoff(uint64_t m, const DeviceWeights& w) {
+    Handoff h;
+    if (!gemm_wide(m, w) || w.input / 64 < 2) return h;
+    const WideSplit sp = wide_split(m, w.output);
+    if (sp.half) return h;
+    const uint64_t tiles = ((m + 255) / 256) * (w.output / 256), rem = tiles % 256;
+    if (tiles < 256 || rem == 0 || rem > 128 || tiles % 8) return h;
+    h.q = uint32_t(tiles / 256);
+    h.x = uint32_t(rem);
+    return h;
+}
+static uint64_t handoff_bytes(uint32_t x) { return uint64_t(x) * 8 * 128 * 64 * sizeof(float); }
+
+// Workspace of one pass of m rows: fragment-order input, then the handoff's
+// partial accumulators and flags.
+static uint64_t pass_workspace(const DeviceWeights& w, uint64_t m) {
+    const Handoff h = gemm_handoff(m, w);
+    return afrag_bytes(w, m) + (h.x ? align256(handoff_bytes(h.x)) + align256(uint64_t(h.x) * 4) : 0);
+}
+
+uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
+    const uint64_t pass = gemm_pass_rows(w);
+    if (rows <= pass) return pass_workspace(w, rows);
+    const uint64_t a = pass_workspace(w, pass), b = rows % pass ? pass_workspace(w, rows % pass) : 0;
+    return a > b ? a : b;
+}
 
 uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows) {
     const uint64_t pass = gemm_pass_rows(w);
@@ -120,12 +156,16 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         const uint32_t rb = wide ? 32 : 16;
         const uint64_t mpad = (m + rb - 1) / rb * rb;
         const float* x = call.x + r0 * call.x_row_stride;
+        const Handoff h = gemm_handoff(m, w);
+        char* hbase = reinterpret_cast<char*>(call.workspace) + afrag_bytes(w, m);
+        float* handoff = reinterpret_cast<float*>(hbase);
+        uint32_t* flags = reinterpret_cast<uint32_t*>(hbase + align256(handoff_bytes(h.x)));
         if (wide)
             hipLaunchKernelGGL(input_stage_frag_kernel<32>, dim3(w.input / 128, uint32_t(mpad / 32)), dim3(256), 0,
-                               stream, x, w.suh, uint32_t(m), w.input, afrag);
+                               stream, x, w.suh, uint32_t(m), w.input, afrag, flags, h.x);
         else
             hipLaunchKernelGGL(input_stage_frag_kernel<16>, dim3(w.input / 128, uint32_t(mpad / 16)), dim3(256), 0,
-                               stream, x, w.suh, uint32_t(m), w.input, afrag);
+                               stream, x, w.suh, uint32_t(m), w.input, afrag, flags, 0u);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         GemmLaunch l{};
@@ -140,6 +180,11 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         l.args.N = w.output;
         l.args.alpha = call.alpha;
         l.args.beta = call.beta;
+        l.args.q = h.q;
+        l.args.x = h.x;
+        l.args.handoff = h.x ? handoff : nullptr;
+        l.args.flags = h.x ? flags : nullptr;
+        l.args.poll_limit = call.handoff_poll_limit;
         l.codebook = w.codebook;
         l.bm = gemm_bm(m, w.output / 128);
         l.stream = stream;

@@ -43,7 +43,13 @@ struct GemmArgs {
     float alpha, beta;
     uint32_t col_block0;      // wide kernel: first column block of the launch,
     uint32_t col_blocks;      // column blocks launched,
-    uint32_t tiles;           // and workgroups (column blocks x row blocks)
+    uint32_t tiles;           // and tiles (column blocks x row blocks)
+    // Wide kernel K-split handoff (x > 0): x tiles of the launch split at half
+    // of K between a head and a tail workgroup, 256 q whole tiles.
+    uint32_t q, x;
+    float* handoff;           // [x][8 waves][128 accumulators][64 lanes]
+    uint32_t* flags;          // [x], 0 at launch
+    uint32_t poll_limit;      // tail's polls before it takes a tile over
 };
 
 // Byte offset of the A fragment (row block rb, 32-channel block kb) of lane l.
@@ -203,11 +209,6 @@ __global__ __launch_bounds__(2 * BM) void gemm_kernel(GemmArgs a) {
         __syncthreads();
     }
 }
-
-// Input stage writing the FP16 core input in MFMA A-fragment order:
-// grid (I/128, ceil(M/16)*16), one wave per (row, 128-block); rows >= M are zero.
-__global__ __launch_bounds__(64) void input_stage_frag_kernel(const float* x, const uint16_t* suh, uint32_t M,
-                                                              uint32_t I, _Float16* afrag);
 
 struct GemmLaunch {
     GemmArgs args;

@@ -44,29 +44,42 @@ __host__ __device__ __forceinline__ uint64_t afrag32_offset(uint32_t rb, uint32_
     return ((uint64_t(rb) * (I / 16) + kb) * 64 + lane) * 16;
 }
 
+// Work items.  Without a handoff every workgroup computes one whole tile.
+// With one (M = 2048 on 4096 -> 12288: 384 tiles for 256 CUs, one workgroup
+// per CU at a time) x tiles are split at half of K: the grid is [x heads]
+// [256 q whole tiles][x tails], dispatched in that order.  A head computes K
+// stages [0, S/2) of its tile and publishes the FP32 accumulators; its CU then
+// takes the next whole tile; a tail, dispatched last, continues the same tile
+// over [S/2, S).  The accumulators carry over exactly, so every output keeps
+// the bits of an unsplit tile, and each CU runs about q + 1/2 tile-times
+// instead of q + 1.
+enum : int { kItemFull = 0, kItemHead = 1, kItemTail = 2 };
+
+// Handoff flags: 0 idle, 1 head published, 2 head abandoned.  The tail polls
+// (bounded; its head was dispatched before it, so the wait ends); when the
+// head is late it takes the tile over from K = 0 instead, and whichever of the
+// two comes second puts the flag back to 0, so it is 0 at the end of every
+// launch.
+constexpr uint32_t kHandoffForceRecompute = 0xFFFFFFFFu;   // poll_limit: always take over
+
 // BN = 256: 8 waves as 2 (M) x 4 (N), each 128 x 64 (4 x 2 MFMA tiles), all
 // eight decode.  BN = 128: 4 (M) x 2 (N), each 64 x 64 (2 x 2 tiles); the
 // stage's B is 8 tiles x 4 blocks, decoded by waves 0..3 (one per SIMD) while
 // waves 4..7 issue empty chunk loads so every wave counts the same vmcnt.
-template <int K, int CB, int BN>
+template <int K, int CB, int BN, bool HANDOFF>
 __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
+    static_assert(!HANDOFF || BN == 256, "the handoff runs on 256 x 256 tiles");
     constexpr int WNW = BN / 64;                         // waves along N
     constexpr int TI = 256 / (8 / WNW) / 32;             // 32-row MFMA tiles per wave
     constexpr int TJ = 2;                                // 32-column MFMA tiles per wave
     constexpr int NT = BN / 16;                          // trellis tiles per stage row
-    extern __shared__ __align__(16) unsigned char smem[];
+    extern __shared__ __align__(16) unsigned char smem[];   // all 160 KiB: no static LDS besides
     unsigned char* abuf = smem;                          // 3 x [8 rb32][4 kb16][64][16 B]
     unsigned char* bbuf = smem + 3 * WIDE_TILE_BYTES;    // 2 x [BN/32 n32][4 kb16][64][16 B]
-    // XCD-aware tile order: workgroup i runs on XCD i % 8 (round-robin
-    // dispatch), and each XCD takes a contiguous run of tiles in row-block-major
-    // order, so the workgroups of one XCD share A row blocks in its own L2.
-    uint32_t t = blockIdx.x;
-    if (a.tiles % 8 == 0) t = (t % 8) * (a.tiles / 8) + t / 8;
-    const int c = t % a.col_blocks + a.col_block0, mb = t / a.col_blocks;   // c: BN-column block
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wm = w / WNW, wn = w % WNW;
     const int jt8 = lane >> 3, g = lane & 7;
-    const uint32_t I = a.I, N = a.N, stages = I / 64;
+    const uint32_t I = a.I, N = a.N, stages = I / 64, half = stages / 2;
 
     constexpr uint32_t tile_bytes = 32u * K;
     const uint32_t row_bytes = (N >> 4) * tile_bytes;
@@ -76,13 +89,72 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     const bool decoder = BN == 256 || w < kDecoders;
     const int dblk = BN == 256 ? w >> 1 : w & 3;         // decode role
     const int dtile = BN == 256 ? 8 * (w & 1) + jt8 : jt8;
+
+    // XCD-aware tile order: workgroup i runs on XCD i % 8 (round-robin
+    // dispatch), and each XCD takes a contiguous run of tiles in row-block-major
+    // order, so the workgroups of one XCD share A row blocks in its own L2.
+    // With the handoff, XCD x owns tiles [x * per_xcd, +per_xcd): 32 q whole
+    // tiles, then x / 8 split ones; every role keeps a tile on its XCD.
+    const uint32_t per_xcd = a.tiles / 8;
+    int kind = kItemFull;
+    uint32_t t, hslot = 0;
+    if constexpr (!HANDOFF) {
+        t = blockIdx.x;
+        if (a.tiles % 8 == 0) t = (t % 8) * per_xcd + t / 8;
+    } else {
+        const uint32_t i = blockIdx.x, whole = 256 * a.q;
+        if (i < a.x || i >= a.x + whole) {
+            kind = i < a.x ? kItemHead : kItemTail;
+            hslot = i < a.x ? i : i - a.x - whole;
+            t = (hslot % 8) * per_xcd + 32 * a.q + hslot / 8;
+        } else {
+            const uint32_t j = i - a.x;
+            t = (j % 8) * per_xcd + j / 8;
+        }
+    }
+    const int c = t % a.col_blocks + a.col_block0, mb = t / a.col_blocks;   // c: BN-column block
     const uint32_t lane_off = (uint32_t(NT) * c + dtile) * tile_bytes + g * 4u * K;
+
+    // Partial accumulators of split tile hslot: element e of wave w's lane l
+    // at [hslot][w][e][l] (coalesced per element).
+    auto hpart = [&]() -> float* { return a.handoff + ((uint64_t(hslot) * 8 + w) * (TI * TJ * 16)) * 64 + lane; };
+
+    // K stages [s0, s_end) of this item.
+    uint32_t s0 = 0, s_end = kind == kItemHead ? half : stages;
+    if (HANDOFF && kind == kItemTail) {
+        if (tid == 0) {
+            uint32_t* flag = a.flags + hslot;
+            int take = 0;
+            if (a.poll_limit != kHandoffForceRecompute) {
+                for (uint32_t spin = 0;; ++spin) {
+                    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u) {
+                        take = 1;
+                        break;
+                    }
+                    if (spin >= a.poll_limit) break;
+                    __builtin_amdgcn_s_sleep(8);
+                }
+            }
+            if (take) {
+                __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                // Abandon: from here on the head's publish fails.  If it was
+                // published in the meantime, this side clears the flag.
+                const uint32_t old = __hip_atomic_exchange(flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (old == 1u) __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            *reinterpret_cast<volatile int*>(smem) = take;
+        }
+        __syncthreads();
+        if (*reinterpret_cast<volatile int*>(smem)) s0 = half;
+        __syncthreads();   // every wave has read it before the prologue's DMAs reuse the word
+    }
 
     // ---- B: chunk ring (stage st in slot st % D), one chunk per lane ----
     constexpr int D = 1;   // chunk ring depth; 2 would spill at 256 VGPRs
     Chunk<K> ring[D];
     auto load_stage = [&](Chunk<K>& dst, uint32_t st) {
-        load_chunk(dst, wrsrc, (decoder && st < stages) ? (st * 4 + dblk) * row_bytes + lane_off : 0x80000000u);
+        load_chunk(dst, wrsrc, (decoder && st < s_end) ? (st * 4 + dblk) * row_bytes + lane_off : 0x80000000u);
     };
     // Lane (tile dtile, chunk g) holds rows 0..15 of tile columns g and g+8 of
     // input block dblk: column n = 16 (dtile % 2) + g (+8) of 32-column block
@@ -108,7 +180,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     // K16 step f%4) of a stage straight into LDS (buffer_load ... lds).  Three
     // A buffers: stage st is issued two stages ahead, into buffer st % 3.
     auto dma_a = [&](uint32_t st) {
-        const uint32_t kb = st < stages ? 4 * st : 0;
+        const uint32_t kb = st < s_end ? 4 * st : 0;
         unsigned char* base = abuf + (st % 3) * WIDE_TILE_BYTES;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -135,24 +207,33 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     };
 
     float16_t acc[TI][TJ];
+    if (!HANDOFF || s0 == 0) {
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = float16_t{};
+            for (int j = 0; j < TJ; ++j) acc[i][j] = float16_t{};
+    } else {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = load_coherent(hpart() + ((i * TJ + j) * 16 + r) * 64);
+    }
 
-    // Prologue: A stages 0 and 1 in flight, B stage 0 decoded, chunk ring full.
+    // Prologue: A stages s0 and s0 + 1 in flight, B stage s0 decoded, chunk ring full.
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_stage(ring[d], d);
+    for (int d = 0; d < D; ++d) load_stage(ring[d], s0 + d);
     __builtin_amdgcn_sched_barrier(0);
-    dma_a(0);
-    dma_a(1);
+    dma_a(s0);
+    dma_a(s0 + 1);
     __builtin_amdgcn_sched_barrier(0);
-    decode_stage(ring[0], 0);
-    load_stage(ring[0], D);
+    decode_stage(ring[0], s0 & 1);
+    load_stage(ring[0], s0 + D);
     __builtin_amdgcn_sched_barrier(0);
-    stage_barrier(std::integral_constant<int, 4 + kChunkOps>{});   // A stage 0 landed
+    stage_barrier(std::integral_constant<int, 4 + kChunkOps>{});   // A stage s0 landed
 
-    for (uint32_t st0 = 0; st0 < stages; st0 += D) {
+    for (uint32_t st0 = s0; st0 < s_end; st0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const uint32_t st = st0 + d;
@@ -206,6 +287,28 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             // last stage's chunk loads, this stage's 4 DMAs and chunk loads remain.
             stage_barrier(std::integral_constant<int, 4 + 2 * kChunkOps>{});
         }
+    }
+    // The last stages issued A DMAs past the end (dummy rows into A buffers):
+    // they land before LDS is reused as the epilogue tile or by the next item.
+    stage_barrier(std::integral_constant<int, 0>{});
+
+    if (HANDOFF && kind == kItemHead) {
+        float* const hp = hpart();
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) store_coherent(hp + ((i * TJ + j) * 16 + r) * 64, acc[i][j][r]);
+        __builtin_amdgcn_s_waitcnt(0);   // every partial store complete
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t expected = 0;
+            if (!__hip_atomic_compare_exchange_strong(a.flags + hslot, &expected, 1u, __ATOMIC_RELAXED,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                __hip_atomic_store(a.flags + hslot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // abandoned
+        }
+        return;
     }
 
     // ---- Epilogue: rows [128 p, +128) through an LDS [128][BN] FP32 tile ----
@@ -267,9 +370,13 @@ hipError_t gemm_wide_dispatch(const GemmLaunch& l);
     template <>                                                                                        \
     hipError_t gemm_wide_dispatch<K>(const GemmLaunch& l) {                                            \
         using Fn = void (*)(GemmArgs);                                                                 \
-        static const Fn table[2][3] = {                                                                \
-            {gemm_wide_kernel<K, 0, 256>, gemm_wide_kernel<K, 1, 256>, gemm_wide_kernel<K, 2, 256>},   \
-            {gemm_wide_kernel<K, 0, 128>, gemm_wide_kernel<K, 1, 128>, gemm_wide_kernel<K, 2, 128>}};  \
+        static const Fn table[3][3] = {                                                                \
+            {gemm_wide_kernel<K, 0, 256, false>, gemm_wide_kernel<K, 1, 256, false>,                   \
+             gemm_wide_kernel<K, 2, 256, false>},                                                      \
+            {gemm_wide_kernel<K, 0, 128, false>, gemm_wide_kernel<K, 1, 128, false>,                   \
+             gemm_wide_kernel<K, 2, 128, false>},                                                      \
+            {gemm_wide_kernel<K, 0, 256, true>, gemm_wide_kernel<K, 1, 256, true>,                     \
+             gemm_wide_kernel<K, 2, 256, true>}};                                                      \
         static const hipError_t attr = [] {                                                            \
             for (const auto& row : table)                                                              \
                 for (Fn f : row) {                                                                     \
@@ -284,7 +391,9 @@ hipError_t gemm_wide_dispatch(const GemmLaunch& l);
         GemmArgs args = l.args;                                                                        \
         args.col_blocks = l.col_blocks;                                                                \
         args.tiles = l.col_blocks * ((l.args.M + 255) / 256);                                          \
-        hipLaunchKernelGGL(table[l.bn == 128][l.codebook], dim3(args.tiles), dim3(512), WIDE_LDS_BYTES, l.stream, args); \
+        const uint32_t wgs = args.x ? args.tiles + args.x : args.tiles;   /* handoff: + x tails */      \
+        const int variant = args.x ? 2 : l.bn == 128 ? 1 : 0;                                          \
+        hipLaunchKernelGGL(table[variant][l.codebook], dim3(wgs), dim3(512), WIDE_LDS_BYTES, l.stream, args); \
         return hipGetLastError();                                                                      \
     }
 

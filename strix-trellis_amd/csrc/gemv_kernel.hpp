@@ -54,16 +54,6 @@ __device__ __forceinline__ GroupWeights group_weights(const GemvArgs& a, int z) 
     return a.table ? a.table[z] : a.w;
 }
 
-// Partial planes cross workgroups (and XCDs, each with its own L2), so they
-// are written and read with agent-scope coherent accesses (sc1): completed
-// stores are visible device-wide without the full-L2 writeback an agent-scope
-// release fence costs.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Output-stage operands of one lane's two columns (128c + lane, +64), loaded
 // ahead of the fold so their latency overlaps the completion round trip.

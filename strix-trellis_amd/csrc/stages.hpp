@@ -17,6 +17,17 @@
 
 namespace stx {
 
+// Partial sums that cross workgroups (and XCDs, each with its own L2) are
+// written and read with agent-scope coherent accesses (sc1): completed
+// stores are visible device-wide without the full-L2 writeback an agent-scope
+// release fence costs.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 constexpr float INV_SQRT128 = 0x1.6a09e6p-4f;   // RN32(1/sqrt(128))
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t bits) {

@@ -127,3 +127,43 @@ def test_gemm_tile_widths_agree(ctx, N):
     ref = linear.matmul_fp32_stages(x.cpu().numpy()[sel], tr, suh, svh, K, "mul1", b, rotated=q)["output_fp32"]
     synth.gate(y.cpu().numpy()[sel], ref)
     w.destroy()
+
+
+@pytest.mark.parametrize("I,N", [(256, 12288), (384, 8448)])
+@pytest.mark.parametrize("take_over", [0, 1])
+def test_gemm_split_tile_handoff(ctx, I, N, take_over):
+    # M = 2048: 384 (12288 columns) or 264 (8448) 256 x 256 tiles, so 128 or 8
+    # of them are split at half of K between two workgroups (I = 384: six K
+    # stages, split 3 + 3).  With take_over the second workgroup always
+    # recomputes the first half itself (the late-head path).  Either way each
+    # row keeps the bits of unsplit tiles: those of the same rows run as 256
+    # rows (256 x 128 tiles) and as 16 rows (128-row kernel).
+    K, M = 4, 2048
+    print(f"gemm handoff M={M} {I}x{N} take_over={take_over}", flush=True)
+    assert ctx.lib.strix_amd_set_gemm_handoff(ctx.handle, take_over) == 0
+    try:
+        tr, suh, svh, b = synth.layer(I, N, K, 170 + I, bias=True)
+        w = runtime.Weights(ctx, tr, suh, svh, b, "mul1")
+        x = torch.from_numpy(synth.activations(M, I, 171)).to(DEV)
+        y = torch.full((M, N), float("nan"), device=DEV)
+        runtime.gemm(w, x, y)
+        plan_y = torch.full((M, N), float("nan"), device=DEV)
+        plan = runtime.LinearPlan(w, x, plan_y, operation="gemm")
+        for _ in range(2):
+            plan_y.fill_(float("nan"))
+            plan.submit()
+            torch.cuda.synchronize()
+            assert torch.equal(plan_y.view(torch.int32), y.view(torch.int32))
+        plan.destroy()
+        for r0, rows in ((1792, 256), (0, 256), (1000, 16)):
+            yr = torch.full((rows, N), float("nan"), device=DEV)
+            runtime.gemm(w, x[r0:r0 + rows].contiguous(), yr)
+            assert torch.equal(yr.view(torch.int32), y[r0:r0 + rows].view(torch.int32)), (r0, rows)
+        torch.cuda.synchronize()
+        sel = np.r_[0:8, 1020:1028, M - 8:M]
+        q = codec.dequantize_rotated(tr, K, "mul1")
+        ref = linear.matmul_fp32_stages(x.cpu().numpy()[sel], tr, suh, svh, K, "mul1", b, rotated=q)["output_fp32"]
+        synth.gate(y.cpu().numpy()[sel], ref)
+        w.destroy()
+    finally:
+        assert ctx.lib.strix_amd_set_gemm_handoff(ctx.handle, 0) == 0
