@@ -67,6 +67,11 @@ hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream
 // waits for the other splits' planes and finishes.  `planes` must hold
 // GEMV_PLANE_EMPTY in every word on entry and does again when the launch ends.
 hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, float* planes, hipStream_t stream);
+// Second launch of a split-K core: folds planes[S][rows][N] (row stride N) in
+// ascending split order from +0, then H32 and the output stage into call.y.
+hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& call, const float* planes, uint32_t splits,
+                               hipStream_t stream);
+
 // Grouped GEMV over `groups` weights of one geometry (table in device memory).
 // single_launch: the planes are call.workspace, dedicated and EMPTY-filled as
 // for launch_gemv_fused; otherwise a finishing kernel folds them.

@@ -81,6 +81,20 @@ static WideSplit wide_split(uint64_t m, uint32_t n) {
 
 static bool gemm_wide(uint64_t m, const DeviceWeights& w) { return m >= 256 && w.output % 256 == 0; }
 
+// K-split of the narrow (M < 256) kernel: N/128 column groups alone leave
+// most CUs idle (96 workgroups on 4096 -> 12288, 40 on 5120^2), so the input
+// splits in S power-of-two parts until the column groups x S reach the 256
+// CUs (S <= 16, whole 128-channel stages per split).  S depends on the layer
+// only, so every row of every M < 256 call has the same bits; it is part of
+// the core's accumulation order (planes folded in ascending split order from
+// +0, as the split GEMV does).
+static uint32_t narrow_splits(const DeviceWeights& w) {
+    const uint32_t groups = w.output / 128, stages = w.input / 128;
+    uint32_t s = 1;
+    while (groups * s < 256 && s < 16 && stages % (2 * s) == 0) s *= 2;
+    return s;
+}
+
 // K-split handoff of a wide pass with only 256 x 256 tiles: T = 256 q + x
 // tiles with 0 < x <= 128 (and T a multiple of the 8 XCDs) launch as x
 // heads, 256 q whole tiles and x tails (one workgroup per CU at a time), so
@@ -102,8 +116,12 @@ static Handoff gemm_handoff(uint64_t m, const DeviceWeights& w) {
 static uint64_t handoff_bytes(uint32_t x) { return uint64_t(x) * 8 * 128 * 64 * sizeof(float); }
 
 // Workspace of one pass of m rows: fragment-order input, then the handoff's
-// partial accumulators and flags.
+// partial accumulators and flags (wide) or the split planes (narrow).
 static uint64_t pass_workspace(const DeviceWeights& w, uint64_t m) {
+    if (!gemm_wide(m, w)) {
+        const uint32_t s = narrow_splits(w);
+        return afrag_bytes(w, m) + (s > 1 ? align256(uint64_t(s) * m * w.output * sizeof(float)) : 0);
+    }
     const Handoff h = gemm_handoff(m, w);
     return afrag_bytes(w, m) + (h.x ? align256(handoff_bytes(h.x)) + align256(uint64_t(h.x) * 4) : 0);
 }
@@ -121,6 +139,7 @@ uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows) {
     for (uint64_t r0 = 0; r0 < rows; r0 += pass) {
         const uint64_t m = rows - r0 < pass ? rows - r0 : pass;
         n += 2;
+        if (!gemm_wide(m, w) && narrow_splits(w) > 1) ++n;   // plane fold
         if (gemm_wide(m, w)) {
             const WideSplit sp = wide_split(m, w.output);
             n += sp.full && sp.half;
@@ -185,12 +204,22 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         l.args.handoff = h.x ? handoff : nullptr;
         l.args.flags = h.x ? flags : nullptr;
         l.args.poll_limit = call.handoff_poll_limit;
+        l.args.splits = wide ? 1 : narrow_splits(w);
+        l.args.planes = reinterpret_cast<float*>(hbase);
         l.codebook = w.codebook;
         l.bm = gemm_bm(m, w.output / 128);
         l.stream = stream;
         if (!wide) {
             e = gemm_table[w.bits - 1](l);
             if (e != hipSuccess) return e;
+            if (l.args.splits > 1) {
+                LinearCall pc = call;
+                pc.rows = m;
+                pc.y = l.args.y;
+                pc.y_row_stride = w.output;
+                e = launch_plane_finish(w, pc, l.args.planes, l.args.splits, stream);
+                if (e != hipSuccess) return e;
+            }
             continue;
         }
         const WideSplit sp = wide_split(m, w.output);

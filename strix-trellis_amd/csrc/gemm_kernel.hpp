@@ -50,6 +50,11 @@ struct GemmArgs {
     float* handoff;           // [x][8 waves][128 accumulators][64 lanes]
     uint32_t* flags;          // [x], 0 at launch
     uint32_t poll_limit;      // tail's polls before it takes a tile over
+    // Narrow kernel K-split: `splits` workgroups along grid z each take I/splits
+    // input channels and write their raw core rows to planes[s][M][N], which a
+    // second launch folds in ascending s from +0 before the output stage.
+    uint32_t splits;
+    float* planes;
 };
 
 // Byte offset of the A fragment (row block rb, 32-channel block kb) of lane l.
@@ -64,15 +69,18 @@ template <int K, int CB, int BM>
 __global__ __launch_bounds__(2 * BM) void gemm_kernel(GemmArgs a) {
     constexpr int WM = BM / 64, NW = 2 * WM, BPW = GEMM_STAGE_BLOCKS / NW;
     extern __shared__ __align__(16) unsigned char smem[];   // 2 B stages; reused by the epilogue
-    const int c = blockIdx.x, mb = blockIdx.y;
+    const int c = blockIdx.x, mb = blockIdx.y, split = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wm = w >> 1, wn = w & 1;
     const int jt = lane >> 3, g = lane & 7;
-    const uint32_t I = a.I, N = a.N, stages = I / 128;
+    // This workgroup's K range: stages (128 channels each) [split * stages, +stages).
+    const uint32_t I = a.I, N = a.N, stages = I / 128 / a.splits, kb0 = uint32_t(split) * stages * 4;
 
     constexpr uint32_t tile_bytes = 32u * K;
     const uint32_t row_bytes = (N >> 4) * tile_bytes;
-    const auto wrsrc = make_rsrc(a.trellis, uint32_t(uint64_t(I / 16) * row_bytes));
+    const auto wrsrc = make_rsrc(reinterpret_cast<const char*>(a.trellis) +
+                                     uint64_t(split) * stages * GEMM_STAGE_BLOCKS * row_bytes,
+                                 uint32_t(uint64_t(stages) * GEMM_STAGE_BLOCKS * row_bytes));
     const auto arsrc = make_rsrc(a.afrag, uint32_t(a.afrag_bytes));
     const uint32_t lane_off = (8u * c + jt) * tile_bytes + g * 4u * K;
 
@@ -119,7 +127,7 @@ __global__ __launch_bounds__(2 * BM) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                arsrc, uint32_t(afrag_offset(rb0 + i, kb32, I, lane)), 0, 0);
+                arsrc, uint32_t(afrag_offset(rb0 + i, kb0 + kb32, I, lane)), 0, 0);
             af[i] = __builtin_bit_cast(half8_t, v);
         }
     };
@@ -175,6 +183,22 @@ __global__ __launch_bounds__(2 * BM) void gemm_kernel(GemmArgs a) {
             load_stage(ring[slot], st + 1 + D);
             __syncthreads();
         }
+    }
+
+    if (a.splits > 1) {
+        // Raw core rows of this split -> its plane (folded by a second launch).
+        float* plane = a.planes + uint64_t(split) * a.M * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t row = uint32_t(mb) * BM + 64 * wm + 16 * i + 4 * (lane >> 4) + e;
+                if (row < a.M) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) plane[uint64_t(row) * N + 128 * c + 64 * wn + 16 * j + (lane & 15)] = acc[i][j][e];
+                }
+            }
+        return;
     }
 
     // Epilogue, 64 rows (one wm) at a time through a [64][128] FP32 LDS tile.
@@ -235,7 +259,7 @@ inline size_t gemm_lds_bytes(int bm) {
         static const Fn t256[3] = {gemm_kernel<K, 0, 256>, gemm_kernel<K, 1, 256>, gemm_kernel<K, 2, 256>}; \
         static const Fn t128[3] = {gemm_kernel<K, 0, 128>, gemm_kernel<K, 1, 128>, gemm_kernel<K, 2, 128>}; \
         const Fn fn = l.bm == 256 ? t256[l.codebook] : t128[l.codebook];                               \
-        const dim3 grid(l.args.N / 128, (l.args.M + l.bm - 1) / l.bm);                                  \
+        const dim3 grid(l.args.N / 128, (l.args.M + l.bm - 1) / l.bm, l.args.splits);                   \
         hipLaunchKernelGGL(fn, grid, dim3(2 * l.bm), gemm_lds_bytes(l.bm), l.stream, l.args);          \
         return hipGetLastError();                                                                       \
     }

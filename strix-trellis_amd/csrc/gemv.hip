@@ -100,6 +100,25 @@ hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream
     return hipGetLastError();
 }
 
+hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& call, const float* planes, uint32_t splits,
+                               hipStream_t stream) {
+    if (!call.rows) return hipSuccess;
+    GemvArgs a{};
+    a.w = {w.trellis, w.suh, w.svh, w.bias};
+    a.y = call.y;
+    a.partials = const_cast<float*>(planes);
+    a.y_row_stride = call.y_row_stride;
+    a.I = w.input;
+    a.N = w.output;
+    a.rows = uint32_t(call.rows);
+    a.splits = splits;
+    a.alpha = call.alpha;
+    a.beta = call.beta;
+    const uint32_t row_groups = uint32_t((call.rows + GEMV_WAVES - 1) / GEMV_WAVES);
+    hipLaunchKernelGGL(gemv_finish_kernel, dim3(w.output / 128, row_groups, 1), dim3(GEMV_THREADS), 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, float* planes, hipStream_t stream) {
     if (!gemv_fits(w)) return hipErrorInvalidValue;
     GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, planes, 1, stream);

@@ -75,11 +75,12 @@ __device__ __forceinline__ ColumnOperands column_operands(const GroupWeights& gw
     return o;
 }
 
-// Output stage of column group c for every row: fold, H32, epilogue.
+// Output stage of column group c for every row: fold, H32, epilogue.  Rows
+// are spread over the waves of the grid's y dimension (one row per wave and
+// step; a grid with gridDim.y == 1 walks all rows in its four waves).
 // `plane(s, r)` returns the pointer to the 128 values of split s, row r.
 // The splits are folded in ascending order from +0; all their loads are
-// issued before the first add (one memory round trip per kFoldBatch splits):
-// a load past the last split re-reads the last plane and is not added.
+// issued before the first add (one memory round trip per kFoldBatch splits).
 template <bool COHERENT, typename Plane>
 __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWeights& gw, const ColumnOperands& op,
                                                float* y, int c, int splits, Plane plane) {
@@ -88,16 +89,17 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
         if constexpr (COHERENT) return load_coherent(p);
         else return *p;
     };
-    for (uint32_t r = w; r < a.rows; r += GEMV_WAVES) {
+    for (uint32_t r = blockIdx.y * GEMV_WAVES + w; r < a.rows; r += gridDim.y * GEMV_WAVES) {
         float z0 = 0.0f, z1 = 0.0f;
         for (int s = 0; s < splits; s += kFoldBatch) {
             float v0[kFoldBatch], v1[kFoldBatch];
 #pragma unroll
             for (int u = 0; u < kFoldBatch; ++u) {
-                const int ss = s + u < splits ? s + u : splits - 1;
-                const float* p = plane(ss, r);
-                v0[u] = load(p + lane);
-                v1[u] = load(p + lane + 64);
+                if (s + u < splits) {
+                    const float* p = plane(s + u, r);
+                    v0[u] = load(p + lane);
+                    v1[u] = load(p + lane + 64);
+                }
             }
 #pragma unroll
             for (int u = 0; u < kFoldBatch; ++u) {

@@ -2,8 +2,10 @@
 
 Bars: the full operator meets the reference GPU gate against the oracle's
 staged FP32 layer (reference docs/GPU_TESTS.md:124-143); the core is within
-max-rel-err 1e-3 of the FP64 product of the same FP16 operands; every row's
-bits are independent of how many rows are submitted with it.
+max-rel-err 1e-3 of the FP64 product of the same FP16 operands; a row's bits
+do not depend on the other rows of the call (only on whether M reaches 256,
+which selects the split-K narrow path or the one-pass wide tiles) nor on the
+tile shape or split-tile handoff that computes it.
 """
 import numpy as np
 import pytest
@@ -74,18 +76,31 @@ def test_gemm_core_within_fp64_tolerance(ctx):
 
 
 def test_gemm_rows_independent_of_batch_and_alpha_beta(ctx):
+    # The core's accumulation order depends on the layer and on whether M
+    # reaches 256 (below: K split in S planes, S fixed by the layer; from 256:
+    # one K pass per tile), never on the other rows of the call.
     I, N, K = 512, 512, 5
     tr, suh, svh, b = synth.layer(I, N, K, 77, bias=True)
     w = runtime.Weights(ctx, tr, suh, svh, b, "mul1")
     x = torch.from_numpy(synth.activations(300, I, 78)).to(DEV)
     y_all = torch.empty((300, N), device=DEV)
     runtime.gemm(w, x, y_all)
+    y256 = torch.empty((256, N), device=DEV)
+    runtime.gemm(w, x[44:].contiguous(), y256)
+    assert torch.equal(y256.view(torch.int32), y_all[44:].view(torch.int32))
+    y200 = torch.empty((200, N), device=DEV)
+    runtime.gemm(w, x[:200].contiguous(), y200)
     y16 = torch.empty((16, N), device=DEV)
     runtime.gemm(w, x[:16].contiguous(), y16)
-    assert torch.equal(y16.view(torch.int32), y_all[:16].view(torch.int32))
+    assert torch.equal(y16.view(torch.int32), y200[:16].view(torch.int32))
     y1 = torch.empty((1, N), device=DEV)
-    runtime.gemm(w, x[299:300].contiguous(), y1)
-    assert torch.equal(y1.view(torch.int32), y_all[299:300].view(torch.int32))
+    runtime.gemm(w, x[199:200].contiguous(), y1)
+    assert torch.equal(y1.view(torch.int32), y200[199:200].view(torch.int32))
+    # both classes within the reference gate of the same staged oracle
+    q = codec.dequantize_rotated(tr, K, "mul1")
+    ref = linear.matmul_fp32_stages(x[:200].cpu().numpy(), tr, suh, svh, K, "mul1", b, rotated=q)["output_fp32"]
+    synth.gate(y200.cpu().numpy(), ref)
+    synth.gate(y_all[:200].cpu().numpy(), ref)
     # alpha / beta epilogue on top of the same core
     old = torch.from_numpy(synth.rng(5).standard_normal((300, N)).astype(np.float32)).to(DEV)
     y_ab = old.clone()
@@ -108,8 +123,8 @@ def test_gemm_rows_independent_of_batch_and_alpha_beta(ctx):
 def test_gemm_tile_widths_agree(ctx, N):
     # M = 2048 over N = 8448 runs 32 column blocks as 256 x 256 tiles and the
     # last as 256 x 128 tiles; N = 8192 fills the 256 CUs with 256 x 256 tiles
-    # only.  256 rows run as 256 x 128 tiles, 16 rows on the 128-row kernel:
-    # every row has the same bits whichever tile computes it.
+    # only.  256 rows run as 256 x 128 tiles: every row has the same bits
+    # whichever tile computes it.
     I, K, M = 256, 4, 2048
     print(f"gemm tile widths M={M} {I}x{N} K={K}", flush=True)
     tr, suh, svh, b = synth.layer(I, N, K, 90 + N, bias=True)
@@ -117,10 +132,9 @@ def test_gemm_tile_widths_agree(ctx, N):
     x = torch.from_numpy(synth.activations(M, I, 93)).to(DEV)
     y = torch.full((M, N), float("nan"), device=DEV)
     runtime.gemm(w, x, y)
-    for rows in (256, 16):
-        yr = torch.full((rows, N), float("nan"), device=DEV)
-        runtime.gemm(w, x[M - rows:].contiguous(), yr)
-        assert torch.equal(yr.view(torch.int32), y[M - rows:].view(torch.int32)), rows
+    yr = torch.full((256, N), float("nan"), device=DEV)
+    runtime.gemm(w, x[M - 256:].contiguous(), yr)
+    assert torch.equal(yr.view(torch.int32), y[M - 256:].view(torch.int32))
     torch.cuda.synchronize()
     sel = np.r_[0:24, 1000:1016, M - 24:M]
     q = codec.dequantize_rotated(tr, K, "mul1")
@@ -137,7 +151,7 @@ def test_gemm_split_tile_handoff(ctx, I, N, take_over):
     # stages, split 3 + 3).  With take_over the second workgroup always
     # recomputes the first half itself (the late-head path).  Either way each
     # row keeps the bits of unsplit tiles: those of the same rows run as 256
-    # rows (256 x 128 tiles) and as 16 rows (128-row kernel).
+    # rows (256 x 128 tiles).
     K, M = 4, 2048
     print(f"gemm handoff M={M} {I}x{N} take_over={take_over}", flush=True)
     assert ctx.lib.strix_amd_set_gemm_handoff(ctx.handle, take_over) == 0
@@ -155,7 +169,7 @@ def test_gemm_split_tile_handoff(ctx, I, N, take_over):
             torch.cuda.synchronize()
             assert torch.equal(plan_y.view(torch.int32), y.view(torch.int32))
         plan.destroy()
-        for r0, rows in ((1792, 256), (0, 256), (1000, 16)):
+        for r0, rows in ((1792, 256), (0, 256), (1000, 256)):
             yr = torch.full((rows, N), float("nan"), device=DEV)
             runtime.gemm(w, x[r0:r0 + rows].contiguous(), yr)
             assert torch.equal(yr.view(torch.int32), y[r0:r0 + rows].view(torch.int32)), (r0, rows)
