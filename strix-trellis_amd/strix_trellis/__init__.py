@@ -5,10 +5,13 @@ the reference's C ABI v1, include/strix_trellis.h).  This package is the thin
 Python host layer over it:
 
 ``abi``      ctypes mirror of the C ABI (descriptors, statuses, library loader);
-``runtime``  contexts, prepared weights, GEMV/GEMM calls, plans (torch device buffers).
+``runtime``  contexts, prepared weights, GEMV/GEMM calls, plans (torch device buffers);
+``loader``   EXL3 groups mapped from local safetensors files and their transport;
+``fixture``  the STGPU001 fixture container (reader and writer).
 """
 from . import abi
 from .abi import StrixError
+from .loader import Exl3Tensor, SafetensorsFile, load_exl3
 
-__all__ = ["abi", "StrixError"]
+__all__ = ["abi", "StrixError", "Exl3Tensor", "SafetensorsFile", "load_exl3"]
 __version__ = "0.3.0"

@@ -122,6 +122,46 @@ class Weights:
         self._blob, self._meta = blob, m
         return self.lib.strix_weights_prepare(self.ctx.handle, C.byref(t), C.byref(sd), C.byref(h))
 
+    @classmethod
+    def from_transport(cls, ctx, group, stream=None, blob=False):
+        """Weights prepared from an EXL3 group's canonical transport (a
+        ``loader.Exl3Tensor``): its borrowed regions through
+        strix_weights_prepare_parts, or with blob=True its blob through
+        strix_weights_prepare.  Preparation copies and synchronises, so the
+        host views may go once this returns."""
+        self = cls.__new__(cls)
+        self.ctx, self.lib = ctx, ctx.lib
+        h = C.c_void_p()
+        sd = stream_desc(stream)
+        if blob:
+            data, meta = group.transport_blob()
+            raw = np.frombuffer(data, dtype=np.uint8)
+            m = abi.Metadata(struct_size=C.sizeof(abi.Metadata), **meta)
+            t = abi.header(abi.TransportDesc, format=abi.TRANSPORT_EXL3_CANONICAL,
+                           transport_version=meta["transport_version"], data=raw.ctypes.data, data_bytes=raw.nbytes,
+                           metadata=C.addressof(m), metadata_bytes=C.sizeof(m), rows=meta["rows"],
+                           columns=meta["columns"])
+            status = self.lib.strix_weights_prepare(ctx.handle, C.byref(t), C.byref(sd), C.byref(h))
+        else:
+            regions, meta = group.transport_regions()
+            parts = abi.header(abi.PartsDesc, transport_version=meta["transport_version"], bits_x2=meta["bits_x2"],
+                               rows=meta["rows"], columns=meta["columns"], codebook=meta["codebook"],
+                               marker=meta["marker"])
+            views = []
+            for name, view in regions.items():
+                if view is not None:
+                    arr = np.frombuffer(view, dtype=np.uint8)
+                    views.append(arr)
+                    setattr(parts, name, abi.HostRegion(arr.ctypes.data, arr.nbytes))
+            status = self.lib.strix_weights_prepare_parts(ctx.handle, C.byref(parts), C.byref(sd), C.byref(h))
+        abi.check(status, "strix_weights_prepare")
+        self.handle = h
+        self.input, self.output = meta["columns"], meta["rows"]
+        self.bits = meta["bits_x2"] // 2
+        self.codebook = group.codebook
+        self._keep = []
+        return self
+
     @property
     def packed_bytes(self):
         return self.input * self.output * self.bits // 8
