@@ -7,11 +7,13 @@ Python host layer over it:
 ``abi``      ctypes mirror of the C ABI (descriptors, statuses, library loader);
 ``runtime``  contexts, prepared weights, GEMV/GEMM calls, plans (torch device buffers);
 ``loader``   EXL3 groups mapped from local safetensors files and their transport;
+``tp``       two-rank tensor-parallel views of EXL3 groups (rank_partition);
 ``fixture``  the STGPU001 fixture container (reader and writer).
 """
 from . import abi
 from .abi import StrixError
 from .loader import Exl3Tensor, SafetensorsFile, load_exl3
+from .tp import rank_partition
 
-__all__ = ["abi", "StrixError", "Exl3Tensor", "SafetensorsFile", "load_exl3"]
+__all__ = ["abi", "StrixError", "Exl3Tensor", "SafetensorsFile", "load_exl3", "rank_partition"]
 __version__ = "0.3.0"

@@ -102,3 +102,35 @@ def test_fixture_routes(ctx, tmp_path, path):
     finally:
         for w in ws:
             w.destroy()
+
+
+@pytest.mark.parametrize("site", ["shared_gate", "shared_down"])
+def test_tp_rank_views_on_device(ctx, site):
+    # Two-rank views prepared through the loader's transport: output halves
+    # concatenate to the whole layer's output, input halves (bias on rank 0)
+    # sum to it, within the reference gate of the whole-layer GPU result.
+    from strix_trellis.tp import SITES, rank_partition
+    I, N, axis, _ = SITES[site]
+    tr, suh, svh, b = synth.layer(I, N, 4, 880, bias=True)
+    g = loader.Exl3Tensor(tr.view(np.int16), suh, svh, 4.0, "mul1", b, "mem", site)
+    full = g.prepare(ctx)
+    ranks = [rank_partition(g, site, r).prepare(ctx) for r in (0, 1)]
+    try:
+        x = torch.from_numpy(synth.activations(4, I, 881)).to(DEV)
+        y = torch.empty((4, N), device=DEV)
+        runtime.gemv(full, x, y)
+        if axis == "output":
+            parts = [torch.empty((4, N // 2), device=DEV) for _ in ranks]
+            for w, p in zip(ranks, parts):
+                runtime.gemv(w, x, p)
+            got = torch.cat(parts, dim=1)
+        else:
+            parts = [torch.empty((4, N), device=DEV) for _ in ranks]
+            for r, (w, p) in enumerate(zip(ranks, parts)):
+                runtime.gemv(w, x[:, r * I // 2:(r + 1) * I // 2].contiguous(), p)
+            got = parts[0] + parts[1]
+        torch.cuda.synchronize()
+        synth.gate(got.cpu().numpy(), y.cpu().numpy())
+    finally:
+        for w in [full] + ranks:
+            w.destroy()
