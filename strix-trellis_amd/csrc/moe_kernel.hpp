@@ -183,6 +183,29 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
     auto offg = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbg + og : kOut; };
     auto offu = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbu + ou : kOut; };
 
+    // Input stages (gate and up have their own suh): one 128-block per wave and
+    // unit.  The wave's first two units are loaded before the weight prefetch:
+    // vector loads complete in issue order, so loads issued after the chunks
+    // would wait for the chunks' HBM round trip.
+    const int hblocks = int(bps) / 8, per_proj = nrows * hblocks, units = 2 * per_proj;
+    auto unit_load = [&](int u) -> InputLoad {
+        const int p = u / per_proj, v = u - p * per_proj;
+        const int i = v / hblocks, hb = v - i * hblocks;
+        const uint32_t r = moe_nth_route(active, i) / a.topk;
+        const uint32_t ch = a0 * 16 + hb * 128;
+        const uint16_t* suh = p ? ex.up.suh : ex.gate.suh;
+        return input_load(a.x + r * a.x_stride + ch, suh + ch, true);
+    };
+    auto unit_out = [&](int u) -> _Float16* {
+        const int p = u / per_proj, v = u - p * per_proj;
+        const int i = v / hblocks, hb = v - i * hblocks;
+        return act + (p * MOE_MAX_RT + i) * act_row + hb * 128;
+    };
+    // Units past the end load unit 0 again (valid addresses, result unused).
+    const InputLoad pre0 = unit_load(w < units ? w : 0);
+    const InputLoad pre1 = unit_load(w + GEMV_WAVES < units ? w + GEMV_WAVES : 0);
+    __builtin_amdgcn_sched_barrier(0);
+
     Chunk<KG> cg[MOE_RING_GU];
     Chunk<KU> cu[MOE_RING_GU];
 #pragma unroll
@@ -191,16 +214,9 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
         load_chunk(cu[u], ru, offu(u));
     }
 
-    // Input stages (gate and up have their own suh): one 128-block per wave and unit.
-    const int hblocks = int(bps) / 8, per_proj = nrows * hblocks;
-    for (int u = w; u < 2 * per_proj; u += GEMV_WAVES) {
-        const int p = u / per_proj, v = u - p * per_proj;
-        const int i = v / hblocks, hb = v - i * hblocks;
-        const uint32_t r = moe_nth_route(active, i) / a.topk;
-        const uint32_t ch = a0 * 16 + hb * 128;
-        const uint16_t* suh = p ? ex.up.suh : ex.gate.suh;
-        input_block(a.x + r * a.x_stride + ch, suh + ch, act + (p * MOE_MAX_RT + i) * act_row + hb * 128, true);
-    }
+    if (w < units) input_compute(pre0, unit_out(w));
+    if (w + GEMV_WAVES < units) input_compute(pre1, unit_out(w + GEMV_WAVES));
+    for (int u = w + 2 * GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
     // Rows past nrows stay unused: dot_block reads only rows < RT and the
     // fold below only rows < nrows; rows nrows..RT-1 hold stale LDS and their
     // sums are discarded.
@@ -314,17 +330,27 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
     constexpr uint32_t kOut = 0x80000000u;
     auto off = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rb + lo : kOut; };
 
+    // Input stage of the hidden rows; the wave's first two units are loaded
+    // ahead of the weight prefetch (see the gate/up core).
+    const int hblocks = int(bps) / 8, units = nrows * hblocks;
+    auto unit_load = [&](int u) -> InputLoad {
+        const int i = u / hblocks, hb = u - i * hblocks;
+        const uint32_t j = moe_nth_route(active, i);
+        const uint32_t ch = a0 * 16 + hb * 128;
+        return input_load(a.hidden + uint64_t(j) * a.H + ch, ex.down.suh + ch, true);
+    };
+    auto unit_out = [&](int u) -> _Float16* { return act + (u / hblocks) * act_row + (u % hblocks) * 128; };
+    const InputLoad pre0 = unit_load(w < units ? w : 0);
+    const InputLoad pre1 = unit_load(w + GEMV_WAVES < units ? w + GEMV_WAVES : 0);
+    __builtin_amdgcn_sched_barrier(0);
+
     Chunk<K> ring[MOE_RING_D];
 #pragma unroll
     for (int u = 0; u < MOE_RING_D; ++u) load_chunk(ring[u], rs, off(u));
 
-    const int hblocks = int(bps) / 8, units = nrows * hblocks;
-    for (int u = w; u < units; u += GEMV_WAVES) {
-        const int i = u / hblocks, hb = u - i * hblocks;
-        const uint32_t j = moe_nth_route(active, i);
-        const uint32_t ch = a0 * 16 + hb * 128;
-        input_block(a.hidden + uint64_t(j) * a.H + ch, ex.down.suh + ch, act + i * act_row + hb * 128, true);
-    }
+    if (w < units) input_compute(pre0, unit_out(w));
+    if (w + GEMV_WAVES < units) input_compute(pre1, unit_out(w + GEMV_WAVES));
+    for (int u = w + 2 * GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
     __syncthreads();
 
     float acc[RT][2];
