@@ -288,3 +288,26 @@ def test_errors_and_empty_rows(ctx):
     assert lib.strix_weights_destroy(w.handle) == abi.STATUS_CODE["INVALID_ARGUMENT"]
     plan.destroy()
     w.destroy()
+
+
+@pytest.mark.parametrize("I,N,K", [(4096, 1024, 5), (3072, 1024, 4), (4096, 2048, 4)])
+def test_single_launch_plan_with_many_splits(ctx, I, N, K):
+    # One row and 17..32 other splits: the last split's workgroup polls the
+    # planes with all four waves and folds them from LDS; same bits as the
+    # two-launch strix_gemv, on every resubmission.
+    w, _ = _weights(ctx, I, N, K, 990 + K, bias=True)
+    bps, splits = w.gemv_shape()
+    print(f"plan {I}x{N} K={K}: {splits} splits", flush=True)
+    assert splits - 1 > 16
+    x = torch.from_numpy(synth.activations(1, I, 991)).to(DEV)
+    ref = torch.empty((1, N), device=DEV)
+    runtime.gemv(w, x, ref)
+    y = torch.empty((1, N), device=DEV)
+    plan = runtime.LinearPlan(w, x, y)
+    for _ in range(3):
+        y.fill_(float("nan"))
+        plan.submit()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+    plan.destroy()
+    w.destroy()
