@@ -73,15 +73,29 @@ __device__ __forceinline__ float moe_swiglu(float g, float u) {
 // ---------------------------------------------------------------------------
 // Route resolution (wave 0; one lane per route j = r*k + slot, rows*k <= 64).
 // ---------------------------------------------------------------------------
+// Route index of the i-th set bit of m (i < popcount(m)).
+__device__ __forceinline__ uint32_t moe_nth_route(uint64_t m, int i) {
+    for (int q = 0; q < i; ++q) m &= m - 1;
+    return uint32_t(__builtin_ctzll(m));
+}
+
 struct MoeGroup {
     uint64_t members;   // valid routes selecting this group's expert
     uint64_t active;    // members with a non-zero score
     uint32_t expert;
-    int leader;         // this workgroup's route leads the group
-    int token_valid;    // the route's token passes every check
+    uint32_t route;     // the group's leader route
+    int leader;         // this workgroup has a group (rank < number of groups)
+    int nan_row;        // else: the invalid token whose NaN rows it writes, or -1
 };
 
-__device__ __forceinline__ void moe_resolve(const MoeArgs& a, uint32_t route, MoeGroup* out) {
+// Workgroup rank r (grid y) takes the r-th expert group in route order: the
+// group led by the r-th leader, a leader being the first route of a valid
+// token to select its expert.  So the workgroups with work form a prefix of the
+// grid, dispatched first and spread evenly over the CUs, instead of sitting
+// wherever their routes happen to lead.  Ranks past the groups take the
+// invalid tokens in order (there are at least as many: an invalid token's k
+// routes lead nothing).  Wave 0, one lane per route.
+__device__ __forceinline__ void moe_resolve(const MoeArgs& a, uint32_t rank, MoeGroup* out) {
     const int lane = threadIdx.x & 63;
     const uint32_t k = a.topk, n = a.rows * k;
     const bool live = uint32_t(lane) < n;
@@ -98,23 +112,36 @@ __device__ __forceinline__ void moe_resolve(const MoeArgs& a, uint32_t route, Mo
     const uint64_t bad = __ballot(live && !ok);
     const uint64_t row_bits = live ? ((1ull << k) - 1) << (row * k) : 0;   // k <= 8, row*k + k <= 64
     const bool tv = live && (bad & row_bits) == 0;
-    const uint32_t e = __shfl(id, int(route), 64);
-    const int tv_route = __shfl(int(tv), int(route), 64);
+    // Leaders: valid routes with no earlier valid route on the same expert.
+    const uint64_t valid = __ballot(tv);
+    bool lead = tv;
+    for (uint32_t q = 0; q < n; ++q) {
+        const uint32_t idq = __builtin_amdgcn_readlane(id, int(q));
+        if (((valid >> q) & 1) && q < uint32_t(lane) && idq == id) lead = false;
+    }
+    const uint64_t leaders = __ballot(lead);
+    const uint32_t groups = uint32_t(__builtin_popcountll(leaders));
+    int nan_row = -1;
+    uint32_t route = 0;
+    if (rank < groups) {
+        route = moe_nth_route(leaders, int(rank));
+    } else {
+        // Invalid tokens: slot 0 of each row whose routes are not valid.
+        const uint64_t firsts = __ballot(live && slot == 0 && !tv);
+        if (rank - groups < uint32_t(__builtin_popcountll(firsts)))
+            nan_row = int(moe_nth_route(firsts, int(rank - groups)) / k);
+    }
+    const uint32_t e = __builtin_amdgcn_readlane(id, int(route));
     const uint64_t members = __ballot(tv && id == e);
     const uint64_t active = members & __ballot(sc != 0.0f);
     if (lane == 0) {
         out->members = members;
         out->active = active;
         out->expert = e;
-        out->token_valid = tv_route;
-        out->leader = tv_route && (members & ((1ull << route) - 1)) == 0;
+        out->route = route;
+        out->leader = rank < groups;
+        out->nan_row = nan_row;
     }
-}
-
-// Route index of the i-th set bit of m (i < popcount(m)).
-__device__ __forceinline__ uint32_t moe_nth_route(uint64_t m, int i) {
-    for (int q = 0; q < i; ++q) m &= m - 1;
-    return uint32_t(__builtin_ctzll(m));
 }
 
 // Fold `splits` planes (stride between splits `step` floats) at p, p+64.
@@ -261,11 +288,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gate_up_kernel(MoeArgs a) {
     float* red = reinterpret_cast<float*>(lds);
     __shared__ MoeGroup grp;
     __shared__ int last;
-    const uint32_t c = blockIdx.x, route = blockIdx.y, split = blockIdx.z;
+    const uint32_t c = blockIdx.x, split = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6;
-    if (w == 0) moe_resolve(a, route, &grp);
+    if (w == 0) moe_resolve(a, blockIdx.y, &grp);
     __syncthreads();
     if (!grp.leader || !grp.active) return;
+    const uint32_t route = grp.route;
     const uint64_t active = grp.active;
     const int nrows = __builtin_popcountll(active);
     const MoeExpert& ex = a.bank[grp.expert];
@@ -385,18 +413,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_down_kernel(MoeArgs a) {
     float* red = reinterpret_cast<float*>(lds);
     __shared__ MoeGroup grp;
     __shared__ uint32_t finish_mask;
-    const uint32_t c = blockIdx.x, route = blockIdx.y, split = blockIdx.z;
+    const uint32_t c = blockIdx.x, split = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
-    if (w == 0) moe_resolve(a, route, &grp);
+    if (w == 0) moe_resolve(a, blockIdx.y, &grp);
     __syncthreads();
-    if (!grp.token_valid) {
-        // One workgroup per (token, column group) writes the NaN row block.
-        if (route % k == 0 && split == 0 && tid < 128)
-            a.y[uint64_t(route / k) * a.y_stride + 128 * c + tid] = __builtin_bit_cast(float, 0x7fc00000u);
+    if (!grp.leader) {
+        // One workgroup per (invalid token, column group) writes its NaN row block.
+        if (grp.nan_row >= 0 && split == 0 && tid < 128)
+            a.y[uint64_t(grp.nan_row) * a.y_stride + 128 * c + tid] = __builtin_bit_cast(float, 0x7fc00000u);
         return;
     }
-    if (!grp.leader) return;
     const uint64_t active = grp.active, members = grp.members;
     const int nrows = __builtin_popcountll(active);
     const MoeExpert& ex = a.bank[grp.expert];
