@@ -79,12 +79,13 @@ __device__ __forceinline__ uint32_t moe_nth_route(uint64_t m, int i) {
     return uint32_t(__builtin_ctzll(m));
 }
 
+// Every field is wave-uniform.
 struct MoeGroup {
     uint64_t members;   // valid routes selecting this group's expert
     uint64_t active;    // members with a non-zero score
     uint32_t expert;
     uint32_t route;     // the group's leader route
-    int leader;         // this workgroup has a group (rank < number of groups)
+    bool leader;        // this workgroup has a group (rank < number of groups)
     int nan_row;        // else: the invalid token whose NaN rows it writes, or -1
 };
 
@@ -94,8 +95,14 @@ struct MoeGroup {
 // grid, dispatched first and spread evenly over the CUs, instead of sitting
 // wherever their routes happen to lead.  Ranks past the groups take the
 // invalid tokens in order (there are at least as many: an invalid token's k
-// routes lead nothing).  Wave 0, one lane per route.
-__device__ __forceinline__ void moe_resolve(const MoeArgs& a, uint32_t rank, MoeGroup* out) {
+// routes lead nothing).  One lane per route; every wave resolves for itself, so
+// the result stays in registers and no barrier is needed to share it.
+//
+// Groups are enumerated in leader order: each pass takes the lowest valid
+// route not yet grouped -- it leads its expert's group, since every lower
+// valid route belongs to an earlier group of another expert -- and removes the
+// whole group with one ballot.  Rank r stops after r + 1 passes.
+__device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank) {
     const int lane = threadIdx.x & 63;
     const uint32_t k = a.topk, n = a.rows * k;
     const bool live = uint32_t(lane) < n;
@@ -112,36 +119,23 @@ __device__ __forceinline__ void moe_resolve(const MoeArgs& a, uint32_t rank, Moe
     const uint64_t bad = __ballot(live && !ok);
     const uint64_t row_bits = live ? ((1ull << k) - 1) << (row * k) : 0;   // k <= 8, row*k + k <= 64
     const bool tv = live && (bad & row_bits) == 0;
-    // Leaders: valid routes with no earlier valid route on the same expert.
     const uint64_t valid = __ballot(tv);
-    bool lead = tv;
-    for (uint32_t q = 0; q < n; ++q) {
-        const uint32_t idq = __builtin_amdgcn_readlane(id, int(q));
-        if (((valid >> q) & 1) && q < uint32_t(lane) && idq == id) lead = false;
+    const uint64_t nonzero = __ballot(sc != 0.0f);
+    uint64_t rest = valid;
+    uint32_t groups = 0;
+    for (; rest; ++groups) {
+        const int lead = __builtin_ctzll(rest);
+        const uint32_t e = __builtin_amdgcn_readlane(id, lead);
+        const uint64_t members = __ballot(id == e) & valid;
+        if (groups == rank) return {members, members & nonzero, e, uint32_t(lead), true, -1};
+        rest &= ~members;
     }
-    const uint64_t leaders = __ballot(lead);
-    const uint32_t groups = uint32_t(__builtin_popcountll(leaders));
+    // Invalid tokens: slot 0 of each row whose routes are not valid.
+    const uint64_t firsts = __ballot(live && slot == 0 && !tv);
     int nan_row = -1;
-    uint32_t route = 0;
-    if (rank < groups) {
-        route = moe_nth_route(leaders, int(rank));
-    } else {
-        // Invalid tokens: slot 0 of each row whose routes are not valid.
-        const uint64_t firsts = __ballot(live && slot == 0 && !tv);
-        if (rank - groups < uint32_t(__builtin_popcountll(firsts)))
-            nan_row = int(moe_nth_route(firsts, int(rank - groups)) / k);
-    }
-    const uint32_t e = __builtin_amdgcn_readlane(id, int(route));
-    const uint64_t members = __ballot(tv && id == e);
-    const uint64_t active = members & __ballot(sc != 0.0f);
-    if (lane == 0) {
-        out->members = members;
-        out->active = active;
-        out->expert = e;
-        out->route = route;
-        out->leader = rank < groups;
-        out->nan_row = nan_row;
-    }
+    if (rank - groups < uint32_t(__builtin_popcountll(firsts)))
+        nan_row = int(moe_nth_route(firsts, int(rank - groups)) / k);
+    return {0, 0, 0, 0, false, nan_row};
 }
 
 // Fold `splits` planes (stride between splits `step` floats) at p, p+64.
@@ -281,17 +275,22 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
     __syncthreads();
 }
 
+// Waves per SIMD the MoE kernels ask the register allocator for: five
+// workgroups per CU where the 2-bit cores fit 96 VGPRs, else four (a 3-bit
+// projection would spill at five).
+constexpr int moe_waves_per_eu(int bits_sum, int projections) { return bits_sum <= 2 * projections ? 5 : 4; }
+
+// LDS is the one activation / partial buffer and nothing else (32 KiB at the
+// largest split), so that five workgroups fit a CU.
 template <int KG, int KU>
-__global__ __launch_bounds__(GEMV_THREADS) void moe_gate_up_kernel(MoeArgs a) {
+__global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(moe_waves_per_eu(KG + KU, 2))))
+void moe_gate_up_kernel(MoeArgs a) {
     __shared__ __align__(16) unsigned char lds[moe_max(MOE_GU_ACT_BYTES, MOE_GU_RED_BYTES)];
     _Float16* act = reinterpret_cast<_Float16*>(lds);
     float* red = reinterpret_cast<float*>(lds);
-    __shared__ MoeGroup grp;
-    __shared__ int last;
     const uint32_t c = blockIdx.x, split = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6;
-    if (w == 0) moe_resolve(a, blockIdx.y, &grp);
-    __syncthreads();
+    const MoeGroup grp = moe_resolve(a, blockIdx.y);
     if (!grp.leader || !grp.active) return;
     const uint32_t route = grp.route;
     const uint64_t active = grp.active;
@@ -313,10 +312,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gate_up_kernel(MoeArgs a) {
         store_coherent(a.p_gu + ((uint64_t(j) * S + split) * 2 + p) * H + 128 * c + n, v);
     }
     moe_release();
+    // The partials in LDS are consumed: word 0 carries the arrival result.
     uint32_t* counter = a.c_gu + uint64_t(route) * (H >> 7) + c;
-    if (tid == 0) last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    int* last = reinterpret_cast<int*>(lds);
+    if (tid == 0) *last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     __syncthreads();
-    if (!last) return;
+    if (!*last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
     // Last split: both output stages, SwiGLU, hidden.
@@ -407,17 +408,16 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
 }
 
 template <int K>
-__global__ __launch_bounds__(GEMV_THREADS) void moe_down_kernel(MoeArgs a) {
+__global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(moe_waves_per_eu(K, 1))))
+void moe_down_kernel(MoeArgs a) {
     __shared__ __align__(16) unsigned char lds[moe_max(MOE_D_ACT_BYTES, MOE_D_RED_BYTES)];
     _Float16* act = reinterpret_cast<_Float16*>(lds);
     float* red = reinterpret_cast<float*>(lds);
-    __shared__ MoeGroup grp;
     __shared__ uint32_t finish_mask;
     const uint32_t c = blockIdx.x, split = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
-    if (w == 0) moe_resolve(a, blockIdx.y, &grp);
-    __syncthreads();
+    const MoeGroup grp = moe_resolve(a, blockIdx.y);
     if (!grp.leader) {
         // One workgroup per (invalid token, column group) writes its NaN row block.
         if (grp.nan_row >= 0 && split == 0 && tid < 128)
