@@ -5,14 +5,14 @@
 // v_dot2 chains, LDS wave fold, coherent partial planes, last-arrival finish)
 // with routed rows instead of a fixed row range:
 //
-//   gate/up : grid (H/128, rows*k, s_gu), 256 threads.  Workgroup (c, j, s)
-//             belongs to route j; it works only if j leads its expert's group
-//             (first valid occurrence in route order).  It gathers the group's
+//   gate/up : grid (H/128, s_gu, rows*k), 256 threads.  Workgroup (c, s, r)
+//             takes the r-th expert group (its leader is the first valid
+//             occurrence of the expert in route order).  It gathers the group's
 //             non-zero-score token rows of X, streams gate AND up tiles of
 //             column group c over input split s and writes both partial
 //             planes; the last split to arrive folds them, applies both output
 //             stages and SwiGLU and writes hidden[r, slot, 128c .. 128c+127].
-//   down    : grid (I/128, rows*k, s_d).  The group leader streams the down
+//   down    : grid (I/128, s_d, rows*k).  The group leader streams the down
 //             tiles once for all its rows (input = hidden of each row) and
 //             writes one plane per row; every workgroup of a group then
 //             arrives at the counter of each member token.  The last arrival
@@ -89,11 +89,12 @@ struct MoeGroup {
     int nan_row;        // else: the invalid token whose NaN rows it writes, or -1
 };
 
-// Workgroup rank r (grid y) takes the r-th expert group in route order: the
-// group led by the r-th leader, a leader being the first route of a valid
-// token to select its expert.  So the workgroups with work form a prefix of the
-// grid, dispatched first and spread evenly over the CUs, instead of sitting
-// wherever their routes happen to lead.  Ranks past the groups take the
+// Workgroup rank r (grid z, the slowest dimension) takes the r-th expert group
+// in route order: the group led by the r-th leader, a leader being the first
+// route of a valid token to select its expert.  So the workgroups with work
+// form one prefix of the grid over all column groups and splits, dispatched
+// first and spread evenly over the CUs, instead of sitting wherever their
+// routes happen to lead.  Ranks past the groups take the
 // invalid tokens in order (there are at least as many: an invalid token's k
 // routes lead nothing).  One lane per route; every wave resolves for itself, so
 // the result stays in registers and no barrier is needed to share it.
@@ -288,9 +289,9 @@ void moe_gate_up_kernel(MoeArgs a) {
     __shared__ __align__(16) unsigned char lds[moe_max(MOE_GU_ACT_BYTES, MOE_GU_RED_BYTES)];
     _Float16* act = reinterpret_cast<_Float16*>(lds);
     float* red = reinterpret_cast<float*>(lds);
-    const uint32_t c = blockIdx.x, split = blockIdx.z;
+    const uint32_t c = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6;
-    const MoeGroup grp = moe_resolve(a, blockIdx.y);
+    const MoeGroup grp = moe_resolve(a, blockIdx.z);
     if (!grp.leader || !grp.active) return;
     const uint32_t route = grp.route;
     const uint64_t active = grp.active;
@@ -414,10 +415,10 @@ void moe_down_kernel(MoeArgs a) {
     _Float16* act = reinterpret_cast<_Float16*>(lds);
     float* red = reinterpret_cast<float*>(lds);
     __shared__ uint32_t finish_mask;
-    const uint32_t c = blockIdx.x, split = blockIdx.z;
+    const uint32_t c = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
-    const MoeGroup grp = moe_resolve(a, blockIdx.y);
+    const MoeGroup grp = moe_resolve(a, blockIdx.z);
     if (!grp.leader) {
         // One workgroup per (invalid token, column group) writes its NaN row block.
         if (grp.nan_row >= 0 && split == 0 && tid < 128)
@@ -499,7 +500,7 @@ void moe_down_kernel(MoeArgs a) {
 #define STX_INSTANTIATE_MOE(KG)                                                                                   \
     template <>                                                                                                   \
     hipError_t moe_gate_up_dispatch<KG>(const MoeArgs& a, hipStream_t s) {                                        \
-        const dim3 grid(a.H / 128, a.rows * a.topk, a.s_gu);                                                      \
+        const dim3 grid(a.H / 128, a.s_gu, a.rows * a.topk);                                                      \
         if (a.up_bits == 2)                                                                                       \
             hipLaunchKernelGGL((moe_gate_up_kernel<KG, 2>), grid, dim3(GEMV_THREADS), 0, s, a);                     \
         else                                                                                                      \
@@ -508,7 +509,7 @@ void moe_down_kernel(MoeArgs a) {
     }                                                                                                             \
     template <>                                                                                                   \
     hipError_t moe_down_dispatch<KG>(const MoeArgs& a, hipStream_t s) {                                           \
-        hipLaunchKernelGGL(moe_down_kernel<KG>, dim3(a.I / 128, a.rows * a.topk, a.s_d), dim3(GEMV_THREADS), 0, s, \
+        hipLaunchKernelGGL(moe_down_kernel<KG>, dim3(a.I / 128, a.s_d, a.rows * a.topk), dim3(GEMV_THREADS), 0, s, \
                            a);                                                                                    \
         return hipGetLastError();                                                                                 \
     }
