@@ -139,6 +139,23 @@ __device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank)
     return {0, 0, 0, 0, false, nan_row};
 }
 
+// The group with every field read from the first lane: the values are uniform
+// already, but the compiler cannot prove it through the resolution loop, and
+// without this the expert's buffer descriptors would sit in VGPRs and every
+// weight load would run a per-lane descriptor loop.
+__device__ __forceinline__ uint32_t moe_first(uint32_t v) { return uint32_t(__builtin_amdgcn_readfirstlane(int(v))); }
+__device__ __forceinline__ uint64_t moe_first(uint64_t v) {
+    return uint64_t(moe_first(uint32_t(v))) | (uint64_t(moe_first(uint32_t(v >> 32))) << 32);
+}
+// A weight base pointer read from the bank (a vector load) as a uniform value.
+__device__ __forceinline__ const char* moe_first_ptr(const uint32_t* p) {
+    return reinterpret_cast<const char*>(moe_first(uint64_t(reinterpret_cast<uintptr_t>(p))));
+}
+__device__ __forceinline__ MoeGroup moe_uniform(const MoeGroup& g) {
+    return {moe_first(g.members), moe_first(g.active), moe_first(g.expert), moe_first(g.route),
+            moe_first(uint32_t(g.leader)) != 0, int(moe_first(uint32_t(g.nan_row)))};
+}
+
 // Fold `splits` planes (stride between splits `step` floats) at p, p+64.
 __device__ __forceinline__ void moe_fold(const float* p, uint32_t splits, uint64_t step, float& z0, float& z1) {
     const int lane = threadIdx.x & 63;
@@ -197,8 +214,8 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
     const uint32_t act_row = bps * 16;
     constexpr uint32_t tg = 32u * KG, tu = 32u * KU;
     const uint32_t rbg = (a.H >> 4) * tg, rbu = (a.H >> 4) * tu;
-    const auto rg = make_rsrc(reinterpret_cast<const char*>(ex.gate.trellis) + uint64_t(a0) * rbg, bps * rbg);
-    const auto ru = make_rsrc(reinterpret_cast<const char*>(ex.up.trellis) + uint64_t(a0) * rbu, bps * rbu);
+    const auto rg = make_rsrc(moe_first_ptr(ex.gate.trellis) + uint64_t(a0) * rbg, bps * rbg);
+    const auto ru = make_rsrc(moe_first_ptr(ex.up.trellis) + uint64_t(a0) * rbu, bps * rbu);
     const uint32_t og = (8u * c + jt) * tg + g * 4u * KG, ou = (8u * c + jt) * tu + g * 4u * KU;
     const int nb = int(bps) / GEMV_WAVES;
     constexpr uint32_t kOut = 0x80000000u;
@@ -291,7 +308,7 @@ void moe_gate_up_kernel(MoeArgs a) {
     float* red = reinterpret_cast<float*>(lds);
     const uint32_t c = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6;
-    const MoeGroup grp = moe_resolve(a, blockIdx.z);
+    const MoeGroup grp = moe_uniform(moe_resolve(a, blockIdx.z));
     if (!grp.leader || !grp.active) return;
     const uint32_t route = grp.route;
     const uint64_t active = grp.active;
@@ -354,7 +371,7 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
     const uint32_t act_row = bps * 16;
     constexpr uint32_t tb = 32u * K;
     const uint32_t rb = (a.I >> 4) * tb;
-    const auto rs = make_rsrc(reinterpret_cast<const char*>(ex.down.trellis) + uint64_t(a0) * rb, bps * rb);
+    const auto rs = make_rsrc(moe_first_ptr(ex.down.trellis) + uint64_t(a0) * rb, bps * rb);
     const uint32_t lo = (8u * c + jt) * tb + g * 4u * K;
     const int nb = int(bps) / GEMV_WAVES;
     constexpr uint32_t kOut = 0x80000000u;
@@ -418,7 +435,7 @@ void moe_down_kernel(MoeArgs a) {
     const uint32_t c = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
-    const MoeGroup grp = moe_resolve(a, blockIdx.z);
+    const MoeGroup grp = moe_uniform(moe_resolve(a, blockIdx.z));
     if (!grp.leader) {
         // One workgroup per (invalid token, column group) writes its NaN row block.
         if (grp.nan_row >= 0 && split == 0 && tid < 128)
