@@ -37,6 +37,13 @@ strix_status strix_amd_output_stage(strix_weights weights, const float *core, ui
 strix_status strix_amd_gemv_shape(strix_weights weights, uint32_t *blocks_per_split,
     uint32_t *splits);
 
+/* K split of the prefill GEMM core for a call of `rows` rows (its first pass
+ * when the rows run in several): 1 = one K pass per output tile, S > 1 = S
+ * partial planes folded in ascending order.  Like the GEMV shape it fixes the
+ * accumulation order: S depends on the weight geometry and, from 256 rows, on
+ * the number of 256-row blocks.  rows = 0 reports the split of one row. */
+strix_status strix_amd_gemm_splits(strix_weights weights, uint64_t rows, uint32_t *splits);
+
 /* Kernel launches one submission of a prepared plan enqueues (1 for a
  * single-launch GEMV plan). */
 strix_status strix_amd_plan_launches(strix_linear_plan plan, uint32_t *launches);

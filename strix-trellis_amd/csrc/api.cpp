@@ -686,6 +686,13 @@ strix_status strix_amd_gemv_shape(strix_weights w, uint32_t* bps, uint32_t* spli
     return STRIX_SUCCESS;
 }
 
+strix_status strix_amd_gemm_splits(strix_weights w, uint64_t rows, uint32_t* splits) {
+    if (splits) *splits = 0;
+    if (!w || !splits) return STRIX_ERROR_INVALID_ARGUMENT;
+    *splits = stx::gemm_split_count(w->dev, rows ? rows : 1);
+    return STRIX_SUCCESS;
+}
+
 strix_status strix_amd_plan_launches(strix_linear_plan p, uint32_t* launches) {
     if (launches) *launches = 0;
     if (!p || !launches) return STRIX_ERROR_INVALID_ARGUMENT;

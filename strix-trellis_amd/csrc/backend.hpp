@@ -82,6 +82,8 @@ hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights
 // MFMA core with the fused output stage.
 hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
 uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows);
+// K split of the GEMM core for the first pass of a `rows`-row call (1: none).
+uint32_t gemm_split_count(const DeviceWeights& w, uint64_t rows);
 uint32_t linear_launch_count(const DeviceWeights& w, uint64_t rows, bool gemm, bool single_launch);
 // Dispatch used by strix_gemv / strix_gemm / grouped MoE.
 hipError_t launch_linear(const DeviceWeights& w, const LinearCall& call, bool prefer_gemm, hipStream_t stream);

@@ -62,24 +62,47 @@ static uint64_t afrag_bytes(const DeviceWeights& w, uint64_t m) {
     return align256(((m + 31) / 32) * 32 * w.input * 2);   // rows padded for either fragment order
 }
 
-// Column split of a wide pass over the 256 CUs (one 512-thread workgroup per
-// CU): `full` 256-column blocks run as 256 x 256 tiles, `half` as 256 x 128
-// tiles, twice the workgroups at half the work each.  A 256 x 128 tile takes
-// ~0.8 of a 256 x 256 tile's time (measured: the stage barrier and the A
-// stream do not shrink with it), so the narrow tiles are used only when all of
-// them fit one wave of workgroups and the wide ones would leave half the CUs
-// idle (M = 512 on 4096 -> 12288: 130 -> 115 us).
+// Column split and K split of a wide pass over the 256 CUs (one 512-thread
+// workgroup per CU).  `full` 256-column blocks run as 256 x 256 tiles, `half`
+// as 256 x 128 tiles, twice the workgroups at half the work each; a 256 x 128
+// tile takes ~0.8 of a 256 x 256 tile's time (the stage barrier and the A
+// stream do not shrink with it).  A pass whose tiles fill at most half the CUs
+// splits K (below), and there the full tiles win once eight splits or fewer
+// fill the CUs (tiles >= 32; measured on M = 256..768 of 5120^2 and 4096 ->
+// 12288, e.g. M = 512 on 4096 -> 12288: 110 -> 108 us, M = 256: 72 -> 64 us):
+// the plane traffic grows with S, so 20 tiles (M = 256 on 5120^2) stay half
+// tiles at half the split count.  A layer too short to split takes the half
+// tiles whenever all of them fit one wave of workgroups.
 struct WideSplit {
     uint32_t full, half;   // 256-column blocks of each width
 };
-static WideSplit wide_split(uint64_t m, uint32_t n) {
+constexpr uint32_t kWideSplitMinStages = 8;   // 64-channel stages per K split, at least
+static bool wide_can_split(const DeviceWeights& w) { return (w.input / 64) / kWideSplitMinStages >= 2; }
+static WideSplit wide_split(uint64_t m, const DeviceWeights& w) {
     constexpr uint64_t kCus = 256;
-    const uint64_t mb = (m + 255) / 256, nc = n / 256, tiles = mb * nc;
-    if (2 * tiles <= kCus) return {0, uint32_t(nc)};
+    const uint64_t mb = (m + 255) / 256, nc = w.output / 256, tiles = mb * nc;
+    if (2 * tiles <= kCus && (!wide_can_split(w) || 8 * tiles < kCus)) return {0, uint32_t(nc)};
     return {uint32_t(nc), 0};
 }
 
 static bool gemm_wide(uint64_t m, const DeviceWeights& w) { return m >= 256 && w.output % 256 == 0; }
+
+// K split of a wide pass (no handoff) whose workgroups fill at most half of
+// the 256 CUs, e.g. M = 256..768 on 5120^2 (20 to 60 tiles): S workgroups per
+// tile, as many as one round holds, each over at least eight 64-channel
+// stages.  The planes add 2 S M N floats of traffic (written, then folded).
+// S depends on the layer and on the number of 256-row blocks, so rows of calls
+// in the same class share bits.
+static uint32_t wide_splits(uint64_t m, const DeviceWeights& w) {
+    if (!gemm_wide(m, w)) return 1;
+    const WideSplit sp = wide_split(m, w);
+    const uint64_t wgs = ((m + 255) / 256) * (uint64_t(sp.full) + 2 * uint64_t(sp.half));
+    if (2 * wgs > 256) return 1;
+    uint64_t s = 256 / wgs;
+    const uint64_t cap = (w.input / 64) / kWideSplitMinStages;
+    if (s > cap) s = cap;
+    return s > 1 ? uint32_t(s) : 1;
+}
 
 // K-split of the narrow (M < 256) kernel: N/128 column groups alone leave
 // most CUs idle (96 workgroups on 4096 -> 12288, 40 on 5120^2), so the input
@@ -105,7 +128,7 @@ struct Handoff {
 static Handoff gemm_handoff(uint64_t m, const DeviceWeights& w) {
     Handoff h;
     if (!gemm_wide(m, w) || w.input / 64 < 2) return h;
-    const WideSplit sp = wide_split(m, w.output);
+    const WideSplit sp = wide_split(m, w);
     if (sp.half) return h;
     const uint64_t tiles = ((m + 255) / 256) * (w.output / 256), rem = tiles % 256;
     if (tiles < 256 || rem == 0 || rem > 128 || tiles % 8) return h;
@@ -123,7 +146,9 @@ static uint64_t pass_workspace(const DeviceWeights& w, uint64_t m) {
         return afrag_bytes(w, m) + (s > 1 ? align256(uint64_t(s) * m * w.output * sizeof(float)) : 0);
     }
     const Handoff h = gemm_handoff(m, w);
-    return afrag_bytes(w, m) + (h.x ? align256(handoff_bytes(h.x)) + align256(uint64_t(h.x) * 4) : 0);
+    const uint32_t s = wide_splits(m, w);
+    return afrag_bytes(w, m) + (h.x ? align256(handoff_bytes(h.x)) + align256(uint64_t(h.x) * 4) : 0) +
+           (s > 1 ? align256(uint64_t(s) * m * w.output * sizeof(float)) : 0);
 }
 
 uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
@@ -141,11 +166,17 @@ uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows) {
         n += 2;
         if (!gemm_wide(m, w) && narrow_splits(w) > 1) ++n;   // plane fold
         if (gemm_wide(m, w)) {
-            const WideSplit sp = wide_split(m, w.output);
+            const WideSplit sp = wide_split(m, w);
             n += sp.full && sp.half;
+            if (wide_splits(m, w) > 1) ++n;   // plane fold
         }
     }
     return n;
+}
+
+uint32_t gemm_split_count(const DeviceWeights& w, uint64_t rows) {
+    const uint64_t pass = gemm_pass_rows(w), m = rows < pass ? rows : pass;
+    return gemm_wide(m, w) ? wide_splits(m, w) : narrow_splits(w);
 }
 
 using GemmDispatch = hipError_t (*)(const GemmLaunch&);
@@ -204,25 +235,27 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         l.args.handoff = h.x ? handoff : nullptr;
         l.args.flags = h.x ? flags : nullptr;
         l.args.poll_limit = call.handoff_poll_limit;
-        l.args.splits = wide ? 1 : narrow_splits(w);
-        l.args.planes = reinterpret_cast<float*>(hbase);
+        l.args.splits = wide ? wide_splits(m, w) : narrow_splits(w);
+        l.args.planes = reinterpret_cast<float*>(hbase);   // a split pass has no handoff
         l.codebook = w.codebook;
         l.bm = gemm_bm(m, w.output / 128);
         l.stream = stream;
+        auto fold_planes = [&]() -> hipError_t {
+            if (l.args.splits == 1) return hipSuccess;
+            LinearCall pc = call;
+            pc.rows = m;
+            pc.y = l.args.y;
+            pc.y_row_stride = w.output;
+            return launch_plane_finish(w, pc, l.args.planes, l.args.splits, stream);
+        };
         if (!wide) {
             e = gemm_table[w.bits - 1](l);
             if (e != hipSuccess) return e;
-            if (l.args.splits > 1) {
-                LinearCall pc = call;
-                pc.rows = m;
-                pc.y = l.args.y;
-                pc.y_row_stride = w.output;
-                e = launch_plane_finish(w, pc, l.args.planes, l.args.splits, stream);
-                if (e != hipSuccess) return e;
-            }
+            e = fold_planes();
+            if (e != hipSuccess) return e;
             continue;
         }
-        const WideSplit sp = wide_split(m, w.output);
+        const WideSplit sp = wide_split(m, w);
         if (sp.full) {
             l.bn = 256;
             l.col_blocks = sp.full;
@@ -237,6 +270,8 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
             e = gemm_wide_table[w.bits - 1](l);
             if (e != hipSuccess) return e;
         }
+        e = fold_planes();
+        if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }

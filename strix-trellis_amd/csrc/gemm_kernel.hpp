@@ -50,9 +50,10 @@ struct GemmArgs {
     float* handoff;           // [x][8 waves][128 accumulators][64 lanes]
     uint32_t* flags;          // [x], 0 at launch
     uint32_t poll_limit;      // tail's polls before it takes a tile over
-    // Narrow kernel K-split: `splits` workgroups along grid z each take I/splits
-    // input channels and write their raw core rows to planes[s][M][N], which a
-    // second launch folds in ascending s from +0 before the output stage.
+    // K split: `splits` workgroups per tile (narrow kernel: grid z, I/splits
+    // channels each; wide kernel: grid y, stage ranges) write their raw core
+    // rows to planes[s][M][N], which a second launch folds in ascending s from
+    // +0 before the output stage.
     uint32_t splits;
     float* planes;
 };

@@ -55,6 +55,11 @@ __host__ __device__ __forceinline__ uint64_t afrag32_offset(uint32_t rb, uint32_
 // instead of q + 1.
 enum : int { kItemFull = 0, kItemHead = 1, kItemTail = 2 };
 
+// K split (no handoff; a pass whose tiles fill at most half the CUs): grid y is
+// the split s, which computes K stages [s * stages / S, (s + 1) * stages / S)
+// of its tile from +0 and writes the raw accumulators to planes[s][M][N]; a
+// second launch folds the planes in ascending s and runs the output stage.
+
 // Handoff flags: 0 idle, 1 head published, 2 head abandoned.  The tail polls
 // (bounded; its head was dispatched before it, so the wait ends); when the
 // head is late it takes the tile over from K = 0 instead, and whichever of the
@@ -120,7 +125,9 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     auto hpart = [&]() -> float* { return a.handoff + ((uint64_t(hslot) * 8 + w) * (TI * TJ * 16)) * 64 + lane; };
 
     // K stages [s0, s_end) of this item.
-    uint32_t s0 = 0, s_end = kind == kItemHead ? half : stages;
+    const uint32_t split = HANDOFF ? 0 : blockIdx.y;
+    uint32_t s0 = HANDOFF ? 0 : uint32_t(uint64_t(split) * stages / a.splits);
+    uint32_t s_end = HANDOFF ? (kind == kItemHead ? half : stages) : uint32_t(uint64_t(split + 1) * stages / a.splits);
     if (HANDOFF && kind == kItemTail) {
         if (tid == 0) {
             uint32_t* flag = a.flags + hslot;
@@ -292,6 +299,21 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     // they land before LDS is reused as the epilogue tile or by the next item.
     stage_barrier(std::integral_constant<int, 0>{});
 
+    if (!HANDOFF && a.splits > 1) {
+        float* const plane = a.planes + uint64_t(split) * a.M * N;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = uint32_t(mb) * 256 + 32 * TI * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    const uint32_t col = uint32_t(BN) * c + 64 * wn + 32 * j + (lane & 31);
+                    if (row < a.M) plane[uint64_t(row) * N + col] = acc[i][j][r];
+                }
+        return;
+    }
+
     if (HANDOFF && kind == kItemHead) {
         float* const hp = hpart();
 #pragma unroll
@@ -393,7 +415,9 @@ hipError_t gemm_wide_dispatch(const GemmLaunch& l);
         args.tiles = l.col_blocks * ((l.args.M + 255) / 256);                                          \
         const uint32_t wgs = args.x ? args.tiles + args.x : args.tiles;   /* handoff: + x tails */      \
         const int variant = args.x ? 2 : l.bn == 128 ? 1 : 0;                                          \
-        hipLaunchKernelGGL(table[variant][l.codebook], dim3(wgs), dim3(512), WIDE_LDS_BYTES, l.stream, args); \
+        if (args.splits < 1 || (args.x && args.splits != 1)) return hipErrorInvalidValue;              \
+        hipLaunchKernelGGL(table[variant][l.codebook], dim3(wgs, args.splits), dim3(512), WIDE_LDS_BYTES, \
+                           l.stream, args);                                                            \
         return hipGetLastError();                                                                      \
     }
 

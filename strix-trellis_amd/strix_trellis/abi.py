@@ -181,6 +181,7 @@ _PROTOTYPES = {
     "strix_amd_output_stage": (_S, [vp, vp, u64, vp, u64, f32, f32, C.POINTER(Stream)]),
     "strix_amd_gemv_shape": (_S, [vp, C.POINTER(u32), C.POINTER(u32)]),
     "strix_amd_plan_launches": (_S, [vp, C.POINTER(u32)]),
+    "strix_amd_gemm_splits": (_S, [vp, u64, C.POINTER(u32)]),
     "strix_amd_swiglu": (_S, [vp, vp, vp, vp, u64, C.POINTER(Stream)]),
     "strix_amd_set_gemm_handoff": (_S, [vp, u32]),
     "strix_tp_dense_plan_create": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), C.POINTER(vp)]),

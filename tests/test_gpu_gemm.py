@@ -3,10 +3,14 @@
 Bars: the full operator meets the reference GPU gate against the oracle's
 staged FP32 layer (reference docs/GPU_TESTS.md:124-143); the core is within
 max-rel-err 1e-3 of the FP64 product of the same FP16 operands; a row's bits
-do not depend on the other rows of the call (only on whether M reaches 256,
-which selects the split-K narrow path or the one-pass wide tiles) nor on the
-tile shape or split-tile handoff that computes it.
+do not depend on the other rows of the call, only on its class: M below 256
+(the split-K narrow path, S fixed by the layer), a wide pass whose tiles fill
+at most half the CUs (K split in S planes, S fixed by the layer and the number
+of 256-row blocks), or one K pass per tile -- and not on the tile shape or
+split-tile handoff that computes it.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -76,9 +80,9 @@ def test_gemm_core_within_fp64_tolerance(ctx):
 
 
 def test_gemm_rows_independent_of_batch_and_alpha_beta(ctx):
-    # The core's accumulation order depends on the layer and on whether M
-    # reaches 256 (below: K split in S planes, S fixed by the layer; from 256:
-    # one K pass per tile), never on the other rows of the call.
+    # The core's accumulation order depends on the layer and on the row class
+    # (below 256: K split in S planes, S fixed by the layer; from 256 on this
+    # eight-stage layer: one K pass per tile), never on the other rows.
     I, N, K = 512, 512, 5
     tr, suh, svh, b = synth.layer(I, N, K, 77, bias=True)
     w = runtime.Weights(ctx, tr, suh, svh, b, "mul1")
@@ -140,6 +144,44 @@ def test_gemm_tile_widths_agree(ctx, N):
     q = codec.dequantize_rotated(tr, K, "mul1")
     ref = linear.matmul_fp32_stages(x.cpu().numpy()[sel], tr, suh, svh, K, "mul1", b, rotated=q)["output_fp32"]
     synth.gate(y.cpu().numpy()[sel], ref)
+    w.destroy()
+
+
+@pytest.mark.parametrize("I,N,K,codebook,splits", [(2432, 512, 4, "mul1", 4), (1280, 256, 5, "3inst", 2),
+                                                    (1024, 8192, 4, "mcg", 2)])
+def test_gemm_wide_k_split(ctx, I, N, K, codebook, splits):
+    # 256 and 300 rows (1 and 2 row blocks) leave most of the 256 CUs idle, so
+    # each tile's K splits in S planes of at least eight 64-channel stages
+    # (I = 2432: 38 stages as 9 + 10 + 9 + 10): N = 512 and 256 run 256 x 128
+    # tiles, N = 8192 (32 and 64 tiles) 256 x 256 ones.  Both calls fall in the
+    # same class, so shared rows keep their bits; the planes fold in ascending
+    # split order before the output stage.
+    print(f"gemm wide K split {I}x{N} K={K} {codebook} S={splits}", flush=True)
+    tr, suh, svh, b = synth.layer(I, N, K, 190 + I, bias=True)
+    w = runtime.Weights(ctx, tr, suh, svh, b, codebook)
+    for rows in (256, 300):
+        got = ctypes.c_uint32()
+        assert ctx.lib.strix_amd_gemm_splits(w.handle, rows, ctypes.byref(got)) == 0
+        assert got.value == splits, (rows, got.value)
+    x = torch.from_numpy(synth.activations(300, I, 191)).to(DEV)
+    y = torch.full((300, N), float("nan"), device=DEV)
+    runtime.gemm(w, x, y)
+    y256 = torch.full((256, N), float("nan"), device=DEV)
+    runtime.gemm(w, x[44:].contiguous(), y256)
+    assert torch.equal(y256.view(torch.int32), y[44:].view(torch.int32))
+    yp = torch.full((300, N), float("nan"), device=DEV)
+    plan = runtime.LinearPlan(w, x, yp, operation="gemm")
+    for _ in range(2):
+        yp.fill_(float("nan"))
+        plan.submit()
+        torch.cuda.synchronize()
+        assert torch.equal(yp.view(torch.int32), y.view(torch.int32))
+    plan.destroy()
+    sel = np.r_[0:8, 120:136, 292:300]
+    q = codec.dequantize_rotated(tr, K, codebook)
+    xs = x.cpu().numpy()[sel]
+    st = linear.matmul_fp32_stages(xs, tr, suh, svh, K, codebook, b, rotated=q)
+    synth.gate(y.cpu().numpy()[sel], st["output_fp32"])
     w.destroy()
 
 
