@@ -156,29 +156,45 @@ __device__ __forceinline__ MoeGroup moe_uniform(const MoeGroup& g) {
             moe_first(uint32_t(g.leader)) != 0, int(moe_first(uint32_t(g.nan_row)))};
 }
 
-// Fold `splits` planes (stride between splits `step` floats) at p, p+64.
-__device__ __forceinline__ void moe_fold(const float* p, uint32_t splits, uint64_t step, float& z0, float& z1) {
+// Fold `splits` planes of two sets p and q (stride between splits `step`
+// floats) at +0 and +64, each from +0 in ascending split order; the loads of
+// both sets are issued together, eight splits at a time.
+__device__ __forceinline__ void moe_fold2(const float* p, const float* q, uint32_t splits, uint64_t step, float& p0,
+                                          float& p1, float& q0, float& q1) {
     const int lane = threadIdx.x & 63;
-    z0 = 0.0f;
-    z1 = 0.0f;
+    p0 = p1 = q0 = q1 = 0.0f;
     uint32_t s = 0;
     for (; s + 8 <= splits; s += 8) {
-        float v0[8], v1[8];
+        float v[4][8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            v0[u] = load_coherent(p + (s + u) * step + lane);
-            v1[u] = load_coherent(p + (s + u) * step + lane + 64);
+            v[0][u] = load_coherent(p + (s + u) * step + lane);
+            v[1][u] = load_coherent(p + (s + u) * step + lane + 64);
+            v[2][u] = load_coherent(q + (s + u) * step + lane);
+            v[3][u] = load_coherent(q + (s + u) * step + lane + 64);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            z0 = z0 + v0[u];
-            z1 = z1 + v1[u];
+            p0 = p0 + v[0][u];
+            p1 = p1 + v[1][u];
+            q0 = q0 + v[2][u];
+            q1 = q1 + v[3][u];
         }
     }
     for (; s < splits; ++s) {
-        z0 = z0 + load_coherent(p + s * step + lane);
-        z1 = z1 + load_coherent(p + s * step + lane + 64);
+        const float a0 = load_coherent(p + s * step + lane), a1 = load_coherent(p + s * step + lane + 64);
+        const float b0 = load_coherent(q + s * step + lane), b1 = load_coherent(q + s * step + lane + 64);
+        p0 = p0 + a0;
+        p1 = p1 + a1;
+        q0 = q0 + b0;
+        q1 = q1 + b1;
     }
+}
+
+// A 64-bit value of lane l (uniform l) as a uniform value.
+__device__ __forceinline__ uint64_t moe_lane64(uint64_t v, int l) {
+    return uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), l))) |
+           (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), l))) << 32);
 }
 
 // Every store of this workgroup is complete before any of its threads goes on
@@ -338,20 +354,27 @@ void moe_gate_up_kernel(MoeArgs a) {
     if (!*last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-    // Last split: both output stages, SwiGLU, hidden.
+    // Last split: both output stages, SwiGLU, hidden.  The output-stage
+    // operands are loaded first, then gate and up planes together, so the
+    // finish waits for about one memory round trip.
     const int lane = tid & 63;
     const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
+    const uint16_t gv0 = ld_global(ex.gate.svh + n0), gv1 = ld_global(ex.gate.svh + n1);
+    const uint16_t uv0 = ld_global(ex.up.svh + n0), uv1 = ld_global(ex.up.svh + n1);
+    const bool gb = ex.gate.bias != nullptr, ub = ex.up.bias != nullptr;
+    const float gb0 = gb ? ld_global(ex.gate.bias + n0) : 0.0f, gb1 = gb ? ld_global(ex.gate.bias + n1) : 0.0f;
+    const float ub0 = ub ? ld_global(ex.up.bias + n0) : 0.0f, ub1 = ub ? ld_global(ex.up.bias + n1) : 0.0f;
     for (int i = w; i < nrows; i += GEMV_WAVES) {
         const uint32_t j = moe_nth_route(active, i);
+        const float* pg = a.p_gu + uint64_t(j) * S * 2 * H + 128 * c;
         float g0, g1, u0, u1;
-        moe_fold(a.p_gu + (uint64_t(j) * S * 2 + 0) * H + 128 * c, S, 2ull * H, g0, g1);
-        moe_fold(a.p_gu + (uint64_t(j) * S * 2 + 1) * H + 128 * c, S, 2ull * H, u0, u1);
+        moe_fold2(pg, pg + H, S, 2ull * H, g0, g1, u0, u1);
         h32_wave(g0, g1);
         h32_wave(u0, u1);
-        g0 = output_element(g0, ld_global(ex.gate.svh + n0), ex.gate.bias, n0, 1.0f, 0.0f, nullptr);
-        g1 = output_element(g1, ld_global(ex.gate.svh + n1), ex.gate.bias, n1, 1.0f, 0.0f, nullptr);
-        u0 = output_element(u0, ld_global(ex.up.svh + n0), ex.up.bias, n0, 1.0f, 0.0f, nullptr);
-        u1 = output_element(u1, ld_global(ex.up.svh + n1), ex.up.bias, n1, 1.0f, 0.0f, nullptr);
+        g0 = output_value(g0, gv0, gb, gb0, 1.0f, 0.0f, nullptr);
+        g1 = output_value(g1, gv1, gb, gb1, 1.0f, 0.0f, nullptr);
+        u0 = output_value(u0, uv0, ub, ub0, 1.0f, 0.0f, nullptr);
+        u1 = output_value(u1, uv1, ub, ub1, 1.0f, 0.0f, nullptr);
         float* hrow = a.hidden + uint64_t(j) * H;
         *(__attribute__((address_space(1))) float*)(hrow + n0) = moe_swiglu(g0, u0);
         *(__attribute__((address_space(1))) float*)(hrow + n1) = moe_swiglu(g1, u1);
@@ -481,25 +504,70 @@ void moe_down_kernel(MoeArgs a) {
     if (!fm) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-    // Tokens whose last arrival this was: ordered slot fold, alpha/beta.
+    // Tokens whose last arrival this was: ordered slot fold, alpha/beta.  Lane
+    // s fetches slot s's score and expert; then the output-stage operands of
+    // every slot and the planes of every slot are loaded together, so a token
+    // waits for about three memory round trips however many slots it has.  A
+    // zero-score slot loads nothing of its expert and adds no term.
     const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
     int q = 0;
     for (uint32_t m = fm; m; m &= m - 1, ++q) {
         if (q % GEMV_WAVES != w) continue;
         const uint32_t r = uint32_t(__builtin_ctz(m));
+        const uint32_t jl = r * k + (uint32_t(lane) < k ? uint32_t(lane) : 0u);
+        const float sc_l = ld_global(a.scores + jl);
+        const MoeExpert& el = a.bank[ld_global(a.ids + jl)];
+        const uint64_t svh_l = reinterpret_cast<uintptr_t>(el.down.svh);
+        const uint64_t bias_l = reinterpret_cast<uintptr_t>(el.down.bias);
+        float sc[MOE_MAX_TOPK], z0[MOE_MAX_TOPK], z1[MOE_MAX_TOPK], b0[MOE_MAX_TOPK], b1[MOE_MAX_TOPK];
+        uint16_t v0[MOE_MAX_TOPK], v1[MOE_MAX_TOPK];
+        bool hb[MOE_MAX_TOPK];
+#pragma unroll
+        for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+            const int sl = uint32_t(s) < k ? s : 0;
+            sc[s] = uint32_t(s) < k ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_l), sl))
+                                    : 0.0f;
+            v0[s] = v1[s] = 0;
+            b0[s] = b1[s] = 0.0f;
+            hb[s] = false;
+            z0[s] = z1[s] = 0.0f;
+            if (sc[s] != 0.0f) {
+                const auto* svh = reinterpret_cast<const uint16_t*>(moe_lane64(svh_l, sl));
+                const auto* bias = reinterpret_cast<const float*>(moe_lane64(bias_l, sl));
+                v0[s] = ld_global(svh + n0);
+                v1[s] = ld_global(svh + n1);
+                hb[s] = bias != nullptr;
+                if (hb[s]) {
+                    b0[s] = ld_global(bias + n0);
+                    b1[s] = ld_global(bias + n1);
+                }
+            }
+        }
+        // Each slot's planes from +0 in ascending split order, all slots per split.
+        for (uint32_t u = 0; u < S; ++u) {
+            float p0[MOE_MAX_TOPK], p1[MOE_MAX_TOPK];
+#pragma unroll
+            for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+                const uint32_t j = r * k + (uint32_t(s) < k ? uint32_t(s) : 0u);
+                const float* p = a.p_d + (uint64_t(j) * S + u) * I + 128 * c;
+                p0[s] = load_coherent(p + lane);
+                p1[s] = load_coherent(p + lane + 64);
+            }
+#pragma unroll
+            for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+                z0[s] = z0[s] + p0[s];
+                z1[s] = z1[s] + p1[s];
+            }
+        }
         float comb0 = 0.0f, comb1 = 0.0f;
-        for (uint32_t s = 0; s < k; ++s) {
-            const uint32_t j = r * k + s;
-            const float score = ld_global(a.scores + j);
-            if (score == 0.0f) continue;
-            const MoeExpert& es = a.bank[ld_global(a.ids + j)];
-            float z0, z1;
-            moe_fold(a.p_d + uint64_t(j) * S * I + 128 * c, S, I, z0, z1);
-            h32_wave(z0, z1);
-            z0 = output_element(z0, ld_global(es.down.svh + n0), es.down.bias, n0, 1.0f, 0.0f, nullptr);
-            z1 = output_element(z1, ld_global(es.down.svh + n1), es.down.bias, n1, 1.0f, 0.0f, nullptr);
-            comb0 = rn32(comb0 + rn32(score * z0));
-            comb1 = rn32(comb1 + rn32(score * z1));
+#pragma unroll
+        for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+            if (sc[s] == 0.0f) continue;   // also every s >= k
+            h32_wave(z0[s], z1[s]);
+            const float y0 = output_value(z0[s], v0[s], hb[s], b0[s], 1.0f, 0.0f, nullptr);
+            const float y1 = output_value(z1[s], v1[s], hb[s], b1[s], 1.0f, 0.0f, nullptr);
+            comb0 = rn32(comb0 + rn32(sc[s] * y0));
+            comb1 = rn32(comb1 + rn32(sc[s] * y1));
         }
         float* yr = a.y + uint64_t(r) * a.y_stride;
         float o0 = rn32(a.alpha * comb0), o1 = rn32(a.alpha * comb1);
