@@ -219,6 +219,22 @@ def test_staged_entry_points_and_validation(ctx):
     plan.down()
     torch.cuda.synchronize()
     assert np.array_equal(y.cpu().numpy().view(np.uint32), full.view(np.uint32))
+    plan.destroy()
+    # a staged down call reads hidden as the caller left it: with hidden
+    # zeroed between the stages every core and (bias-free) output is zero
+    wsp = torch.empty(R * k * H, dtype=torch.float32, device=DEV)
+    plan = runtime.MoePlan(ctx, ws, _dev(x), y, device_ids=_dev(ids.astype(np.int32)), device_scores=_dev(sc),
+                           workspace=wsp)
+    plan.gate_up()
+    wsp.zero_()
+    y.fill_(float("nan"))
+    plan.down()
+    torch.cuda.synchronize()
+    assert not torch.any(y.view(torch.int32) != 0)
+    # and the whole block again matches the two-stage result
+    plan.submit()
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), full.view(np.uint32))
     # weights retained by a plan cannot be destroyed
     assert ctx.lib.strix_weights_destroy(ws[0][0].handle) != 0
     plan.destroy()
