@@ -53,6 +53,59 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
     });
 }
 
+// Fold of the prefill GEMM's K-split planes [S][rows][N] (written by the
+// previous launch) and the output stage: grid (N/128, ceil(rows/16)), each
+// wave four rows.  Per batch of four splits the wave issues all 32 plane loads
+// before the first add, and the four rows' H32 butterflies are interleaved;
+// every row is still folded from +0 in ascending split order, so its bits are
+// those of the one-row-per-wave fold.
+constexpr uint32_t kPlaneRowsPerWave = 4;
+__global__ __launch_bounds__(GEMV_THREADS) void plane_finish_kernel(GemvArgs a) {
+    const int c = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t r0 = (blockIdx.y * GEMV_WAVES + w) * kPlaneRowsPerWave;
+    if (r0 >= a.rows) return;
+    const ColumnOperands op = column_operands(a.w, c);
+    constexpr int P = int(kPlaneRowsPerWave);
+    float z0[P], z1[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) z0[i] = z1[i] = 0.0f;
+    const float* base = a.partials + 128 * c + lane;
+    for (uint32_t s = 0; s < a.splits; s += 4) {
+        float v0[4][P], v1[4][P];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                // Past the last split or row: a valid address again, unused.
+                const uint32_t ss = s + u < a.splits ? s + u : s;
+                const uint32_t r = r0 + i < a.rows ? r0 + i : r0;
+                const float* p = base + (uint64_t(ss) * a.rows + r) * a.N;
+                v0[u][i] = p[0];
+                v1[u][i] = p[64];
+            }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (s + u < a.splits)
+#pragma unroll
+                for (int i = 0; i < P; ++i) {
+                    z0[i] = z0[i] + v0[u][i];
+                    z1[i] = z1[i] + v1[u][i];
+                }
+    }
+    h32_wave_multi<P>(z0, z1);
+    const int n0 = 128 * c + lane, n1 = n0 + 64;
+    const bool has_bias = a.w.bias != nullptr;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        if (r0 + i >= a.rows) break;
+        float* yr = a.y + (r0 + i) * a.y_row_stride;
+        const float o0 = output_value(z0[i], op.sv0, has_bias, op.b0, a.alpha, a.beta, yr + n0);
+        const float o1 = output_value(z1[i], op.sv1, has_bias, op.b1, a.alpha, a.beta, yr + n1);
+        *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+        *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+    }
+}
+
 static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table, uint32_t groups,
                               const LinearCall& call, uint64_t xg, uint64_t yg, float* planes,
                               uint32_t mode, hipStream_t stream) {
@@ -114,8 +167,9 @@ hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& call, c
     a.splits = splits;
     a.alpha = call.alpha;
     a.beta = call.beta;
-    const uint32_t row_groups = uint32_t((call.rows + GEMV_WAVES - 1) / GEMV_WAVES);
-    hipLaunchKernelGGL(gemv_finish_kernel, dim3(w.output / 128, row_groups, 1), dim3(GEMV_THREADS), 0, stream, a);
+    constexpr uint64_t rows_per_wg = GEMV_WAVES * kPlaneRowsPerWave;
+    const uint32_t row_groups = uint32_t((call.rows + rows_per_wg - 1) / rows_per_wg);
+    hipLaunchKernelGGL(plane_finish_kernel, dim3(w.output / 128, row_groups, 1), dim3(GEMV_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
