@@ -20,13 +20,19 @@ __global__ __launch_bounds__(256) void input_stage_frag_kernel(const float* x, c
     if (blk == 0 && rb == 0)
         for (uint32_t i = tid; i < nflags; i += 256) flags[i] = 0;
     const uint32_t ch = blk * 128;
+    // All of the wave's row loads are issued before the first row's arithmetic
+    // (one memory round trip per wave instead of one per row).
+    InputLoad l[RB / 4];
+#pragma unroll
+    for (int q = 0; q < RB / 4; ++q) {
+        const uint32_t row = rb * RB + (RB / 4) * w + q;
+        const bool live = row < M;
+        l[q] = input_load(x + (live ? uint64_t(row) * I : 0) + ch, suh + ch, live);
+    }
 #pragma unroll
     for (int q = 0; q < RB / 4; ++q) {
         const int r = (RB / 4) * w + q;
-        const uint32_t row = rb * RB + r;
-        const bool live = row < M;
-        const InputLoad l = input_load(x + (live ? uint64_t(row) * I : 0) + ch, suh + ch, live);
-        input_values(l, tile[r][lane], tile[r][lane + 64]);
+        input_values(l[q], tile[r][lane], tile[r][lane + 64]);
     }
     __syncthreads();
 #pragma unroll
