@@ -14,7 +14,13 @@ namespace stx {
 GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t /*bits*/) {
     const uint32_t nb = input / 16, nc = output / 128, units = nb / 8;
     constexpr uint32_t target = 512;
-    GemvShape best{8, nb / 8};
+    // When no split count reaches the target (few column groups), 16-block
+    // splits are kept while they leave at least 128 workgroups: 8-block ones
+    // are dominated by each workgroup's fixed costs (4096 -> 1024 alone: 7.8
+    // -> 7.0 us; sixteen of them as the grouped o_a plan: 23.0 -> 20.4 us),
+    // while smaller layers (2048 -> 512) need the workgroups more.
+    GemvShape best = units % 2 == 0 && uint64_t(nc) * (nb / 16) >= 128 ? GemvShape{16, nb / 16}
+                                                                        : GemvShape{8, nb / 8};
     for (uint32_t m = 1; m <= 16; ++m) {
         if (units % m) continue;
         const uint32_t bps = 8 * m, splits = nb / bps;

@@ -290,7 +290,7 @@ def test_errors_and_empty_rows(ctx):
     w.destroy()
 
 
-@pytest.mark.parametrize("I,N,K", [(4096, 1024, 5), (3072, 1024, 4), (4096, 2048, 4)])
+@pytest.mark.parametrize("I,N,K", [(3584, 1024, 5), (3072, 1024, 4), (4096, 2048, 4)])
 def test_single_launch_plan_with_many_splits(ctx, I, N, K):
     # One row and 17..32 other splits: the last split's workgroup polls the
     # planes with all four waves and folds them from LDS; same bits as the
