@@ -182,6 +182,17 @@ def test_gemm_wide_k_split(ctx, I, N, K, codebook, splits):
     xs = x.cpu().numpy()[sel]
     st = linear.matmul_fp32_stages(xs, tr, suh, svh, K, codebook, b, rotated=q)
     synth.gate(y.cpu().numpy()[sel], st["output_fp32"])
+    # alpha / beta on the folded planes: the wide split (300 rows) and the
+    # narrow one (100 rows), each on top of its own alpha = 1, beta = 0 core
+    for rows in (300, 100):
+        xr = x[:rows].contiguous()
+        base = torch.empty((rows, N), device=DEV)
+        runtime.gemm(w, xr, base)
+        old = torch.from_numpy(synth.rng(192 + rows).standard_normal((rows, N)).astype(np.float32)).to(DEV)
+        y_ab = old.clone()
+        runtime.gemm(w, xr, y_ab, alpha=-0.5, beta=2.0)
+        ref = linear.apply_alpha_beta(base.cpu().numpy(), old.cpu().numpy(), -0.5, 2.0)
+        np.testing.assert_array_equal(y_ab.cpu().numpy().view(np.uint32), ref.view(np.uint32))
     w.destroy()
 
 
