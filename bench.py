@@ -284,8 +284,10 @@ def cpu_baseline(sample_seconds=12.0):
     """NumPy oracle (decode + staged FP32 layer) on the north-star layer, host cores.
 
     Phases timed separately: (i) vectorized decode of the packed layer, (ii)
-    the staged FP32 path from x to y given the decoded weights.  NumPy's
-    elementwise work runs on one thread.
+    the staged FP32 path from x to y given the decoded weights -- together the
+    reported rate; NumPy's elementwise work runs on one thread -- and (iii) the
+    FP64 algebraic product with a BLAS matmul, on all of BLAS's threads and on
+    one.
     """
     import numpy as np
     import synth
@@ -308,11 +310,29 @@ def cpu_baseline(sample_seconds=12.0):
             break
     layer = statistics.median(d + s for d, s in zip(dec, stg))
     packed = I * N * K // 8
+
+    def blas_ms():
+        t = []
+        for _ in range(5):
+            a = time.perf_counter()
+            linear.matmul(x, tr, suh, svh, K, rotated=q)
+            t.append(time.perf_counter() - a)
+        return round(statistics.median(t) * 1e3, 2)
+    blas_threads, fp64_all, fp64_one = None, blas_ms(), None
+    try:
+        import threadpoolctl
+        blas_threads = max((i.get("num_threads", 0) for i in threadpoolctl.threadpool_info()
+                            if i.get("user_api") == "blas"), default=None)
+        with threadpoolctl.threadpool_limits(1, user_api="blas"):
+            fp64_one = blas_ms()
+    except ImportError:
+        pass
     return {"value": round(packed / layer / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{len(dec)} full R1 K4 mul1 4096x4096 layers (vectorized decode + staged FP32 path), "
                       f"median {layer * 1e3:.0f} ms per layer",
             "decode_ms": round(statistics.median(dec) * 1e3, 1), "staged_ms": round(statistics.median(stg) * 1e3, 1),
-            "us_per_call": round(layer * 1e6, 1), "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
+            "us_per_call": round(layer * 1e6, 1), "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+            "fp64_blas_ms": fp64_all, "fp64_blas_ms_1_thread": fp64_one, "blas_threads": blas_threads}
 
 
 def _cpu_model():
