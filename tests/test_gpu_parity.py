@@ -188,10 +188,12 @@ def test_rows_plans_and_entry_points_bit_identical(ctx, I, N, K):
         assert torch.equal(yp.view(torch.int32), y8.view(torch.int32))
     assert plan.launches() == 1
     plan.destroy()
-    # 3 rows through the 4-row template keep their bits
-    y3 = torch.empty((3, N), device=DEV)
-    runtime.gemv(w, x[:3].contiguous(), y3)
-    assert torch.equal(y3.view(torch.int32), y8[:3].view(torch.int32))
+    # 3 rows through the 4-row template and 5 or 6 rows through the 6-row
+    # template keep their bits
+    for rows in (3, 5, 6):
+        yr = torch.empty((rows, N), device=DEV)
+        runtime.gemv(w, x[:rows].contiguous(), yr)
+        assert torch.equal(yr.view(torch.int32), y8[:rows].view(torch.int32)), rows
     w.destroy()
 
 
