@@ -186,6 +186,39 @@ __device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeig
     }
 }
 
+// The block activations of every row, read from LDS ahead of the decode (up
+// to four rows, 8 VGPRs each): the decode hides their LDS round trip, which
+// the compiler otherwise places, and waits for, right before the dots
+// (C1 8.26 -> 8.19 us, 5120^2 R1 12.9 -> 12.6 us).
+template <int RT>
+__device__ __forceinline__ void load_act_block(const _Float16* act, uint32_t act_row, u32x4 (&xv)[RT][2]) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(act + r * act_row);
+        xv[r][0] = p[0];
+        xv[r][1] = p[1];
+    }
+}
+template <int RT>
+__device__ __forceinline__ void dot_block_x(const half2_t (&wq)[4][4], const u32x4 (&xv)[RT][2], float (&acc)[RT][2]) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const u32x4 lo = xv[r][0], hi = xv[r][1];
+        const half2_t xp[8] = {as_h2(lo.x), as_h2(lo.y), as_h2(lo.z), as_h2(lo.w),
+                               as_h2(hi.x), as_h2(hi.y), as_h2(hi.z), as_h2(hi.w)};
+        float a0 = acc[r][0], a1 = acc[r][1];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            a0 = __builtin_amdgcn_fdot2(wq[v][0], xp[v], a0, false);
+            a0 = __builtin_amdgcn_fdot2(wq[v][1], xp[v + 4], a0, false);
+            a1 = __builtin_amdgcn_fdot2(wq[v][2], xp[v], a1, false);
+            a1 = __builtin_amdgcn_fdot2(wq[v][3], xp[v + 4], a1, false);
+        }
+        acc[r][0] = a0;
+        acc[r][1] = a1;
+    }
+}
+
 // Dot of one decoded chunk (32 weights: columns g and g+8, rows 0..15 of one
 // input block) with the block's FP16 activations of every row.
 template <int RT>
@@ -290,10 +323,20 @@ void gemv_kernel(GemvArgs a) {
         for (int u = 0; u < 4; ++u) {
             Chunk<K>& slot = ring[u];
             if (t + u < nb) {
-                half2_t wq[4][4];
-                link_chunk(slot, first);
-                decode_chunk<K, CB>(slot, wq);
-                dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+                if constexpr (RT <= 4) {
+                    u32x4 xv[RT][2];
+                    load_act_block<RT>(act + (w + GEMV_WAVES * (t + u)) * 16, act_row, xv);
+                    __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the decode
+                    half2_t wq[4][4];
+                    link_chunk(slot, first);
+                    decode_chunk<K, CB>(slot, wq);
+                    dot_block_x<RT>(wq, xv, acc);
+                } else {
+                    half2_t wq[4][4];
+                    link_chunk(slot, first);
+                    decode_chunk<K, CB>(slot, wq);
+                    dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+                }
             }
             load_chunk(slot, rsrc, block_off(t + u + 4));
         }
