@@ -42,10 +42,10 @@ uint64_t gemv_plane_words(const DeviceWeights& w, uint64_t rows) {
     return sh.splits > 1 ? uint64_t(sh.splits) * rows * w.output : 0;
 }
 
-// Row template of a call: rows are computed in groups of 1, 2, 4, 6 or 8 (the
-// rows past the call's are zero inputs whose results are never stored).  A
-// row's arithmetic does not depend on the template.
-static uint32_t rows_template(uint64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 6 ? 6 : 8; }
+// Row template of a call: rows are computed in groups of 1, 2, 3, 4, 6 or 8
+// (the rows past the call's are zero inputs whose results are never stored).
+// A row's arithmetic does not depend on the template.
+static uint32_t rows_template(uint64_t rows) { return rows <= 4 ? uint32_t(rows ? rows : 1) : rows <= 6 ? 6 : 8; }
 
 using GemvDispatch = hipError_t (*)(const GemvLaunch&);
 static const GemvDispatch gemv_table[8] = {gemv_dispatch<1>, gemv_dispatch<2>, gemv_dispatch<3>,

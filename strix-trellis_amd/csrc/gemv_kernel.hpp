@@ -411,7 +411,7 @@ __global__ __launch_bounds__(64) void decode_kernel(const uint32_t* trellis, uin
 struct GemvLaunch {
     GemvArgs args;
     dim3 grid;
-    uint32_t rows_template;   // 1, 2, 4, 6 or 8
+    uint32_t rows_template;   // 1, 2, 3, 4, 6 or 8
     uint32_t codebook;
     size_t lds;
     hipStream_t stream;
@@ -427,15 +427,15 @@ hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t 
     template <>                                                                                           \
     hipError_t gemv_dispatch<K>(const GemvLaunch& l) {                                                    \
         using Fn = void (*)(GemvArgs);                                                                    \
-        static const Fn table[3][5] = {                                                                   \
-            {gemv_kernel<K, 0, 1>, gemv_kernel<K, 0, 2>, gemv_kernel<K, 0, 4>, gemv_kernel<K, 0, 6>,      \
-             gemv_kernel<K, 0, 8>},                                                                       \
-            {gemv_kernel<K, 1, 1>, gemv_kernel<K, 1, 2>, gemv_kernel<K, 1, 4>, gemv_kernel<K, 1, 6>,      \
-             gemv_kernel<K, 1, 8>},                                                                       \
-            {gemv_kernel<K, 2, 1>, gemv_kernel<K, 2, 2>, gemv_kernel<K, 2, 4>, gemv_kernel<K, 2, 6>,      \
-             gemv_kernel<K, 2, 8>}};                                                                      \
+        static const Fn table[3][6] = {                                                                   \
+            {gemv_kernel<K, 0, 1>, gemv_kernel<K, 0, 2>, gemv_kernel<K, 0, 3>, gemv_kernel<K, 0, 4>,      \
+             gemv_kernel<K, 0, 6>, gemv_kernel<K, 0, 8>},                                                 \
+            {gemv_kernel<K, 1, 1>, gemv_kernel<K, 1, 2>, gemv_kernel<K, 1, 3>, gemv_kernel<K, 1, 4>,      \
+             gemv_kernel<K, 1, 6>, gemv_kernel<K, 1, 8>},                                                 \
+            {gemv_kernel<K, 2, 1>, gemv_kernel<K, 2, 2>, gemv_kernel<K, 2, 3>, gemv_kernel<K, 2, 4>,      \
+             gemv_kernel<K, 2, 6>, gemv_kernel<K, 2, 8>}};                                                \
         const int rt = int(l.rows_template);                                                              \
-        const int ri = rt == 1 ? 0 : rt == 2 ? 1 : rt == 4 ? 2 : rt == 6 ? 3 : 4;                         \
+        const int ri = rt <= 4 ? rt - 1 : rt == 6 ? 4 : 5;                                                \
         hipLaunchKernelGGL(table[l.codebook][ri], l.grid, dim3(GEMV_THREADS), l.lds, l.stream, l.args);   \
         return hipGetLastError();                                                                         \
     }                                                                                                     \

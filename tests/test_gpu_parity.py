@@ -188,8 +188,7 @@ def test_rows_plans_and_entry_points_bit_identical(ctx, I, N, K):
         assert torch.equal(yp.view(torch.int32), y8.view(torch.int32))
     assert plan.launches() == 1
     plan.destroy()
-    # 3 rows through the 4-row template and 5 or 6 rows through the 6-row
-    # template keep their bits
+    # 3 rows (3-row template) and 5 or 6 rows (6-row template) keep their bits
     for rows in (3, 5, 6):
         yr = torch.empty((rows, N), device=DEV)
         runtime.gemv(w, x[:rows].contiguous(), yr)
