@@ -279,9 +279,10 @@ strix_status strix_gemm(strix_context context, const strix_matmul_desc *desc,
     const strix_stream *stream);
 /* Prepared plan: validated once, submitted with no allocation, copy,
  * synchronisation or pointer query (reference include/strix_trellis.h:291-305).
- * A GEMV plan with 1..8 rows runs as ONE kernel launch whose last-arriving
- * workgroup per 128-output group folds the split partials; its completion
- * counters belong to the weights handle and are zeroed at creation. */
+ * A GEMV plan with 1..8 rows runs as ONE kernel launch in which the workgroup
+ * of the last split of each 128-output group folds the other splits' partial
+ * planes; the planes are allocated per plan at creation, owned by the weights
+ * handle, and hold an empty marker between submissions. */
 strix_status strix_linear_plan_create(strix_context context,
     const strix_matmul_desc *desc, const strix_stream *stream,
     uint32_t operation, strix_linear_plan *out);
@@ -293,9 +294,9 @@ strix_status strix_grouped_moe(strix_context context,
     const strix_grouped_moe_desc *desc, const strix_stream *stream);
 
 /* ---- TP dense plans (reference include/strix_trellis.h:314-414) ----
- * Declared for link compatibility; this implementation returns
- * STRIX_ERROR_NOT_IMPLEMENTED from the creators, as a reference build without
- * STRIX_TRELLIS_ENABLE_EXPERIMENTAL_TP does (reference src/tp_api.inc:663-719). */
+ * One TP rank's dense projections on row views (reference src/tp_api.inc:663-719).
+ * Every creator runs the library's decode GEMV, so each output row is
+ * bit-identical to strix_gemv on the same row; the workspace queries return 0. */
 strix_status strix_tp_dense_plan_create(strix_context context,
     const strix_matmul_desc *desc, const strix_stream *stream,
     strix_tp_dense_plan *out);
