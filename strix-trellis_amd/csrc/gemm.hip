@@ -1,5 +1,7 @@
-// Host side of the prefill GEMM and the fragment-order input stage.
+// Host side of the prefill GEMM (launches; the pass, tile-width, K-split and
+// handoff policy is in policy.cpp) and the fragment-order input stage.
 #include "gemm_wide.hpp"
+#include "policy.hpp"
 
 namespace stx {
 
@@ -51,138 +53,6 @@ __global__ __launch_bounds__(256) void input_stage_frag_kernel(const float* x, c
         u32x4* dst = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(afrag) + off);
         *(__attribute__((address_space(1))) u32x4*)(dst) = v;
     }
-}
-
-// Rows per GEMM pass: the fragment buffer of one pass stays below 1 GiB so
-// its buffer resource (32-bit range) and the workspace stay bounded.
-static uint64_t gemm_pass_rows(const DeviceWeights& w) {
-    const uint64_t per_row = uint64_t(w.input) * 2;
-    uint64_t rows = (uint64_t(1) << 30) / per_row;
-    rows -= rows % 256;
-    return rows < 256 ? 256 : rows;
-}
-
-static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
-
-static uint64_t afrag_bytes(const DeviceWeights& w, uint64_t m) {
-    return align256(((m + 31) / 32) * 32 * w.input * 2);   // rows padded for either fragment order
-}
-
-// Column split and K split of a wide pass over the 256 CUs (one 512-thread
-// workgroup per CU).  `full` 256-column blocks run as 256 x 256 tiles, `half`
-// as 256 x 128 tiles, twice the workgroups at half the work each; a 256 x 128
-// tile takes ~0.8 of a 256 x 256 tile's time (the stage barrier and the A
-// stream do not shrink with it).  A pass whose tiles fill at most half the CUs
-// splits K (below), and there the full tiles win once eight splits or fewer
-// fill the CUs (tiles >= 32; measured on M = 256..768 of 5120^2 and 4096 ->
-// 12288, e.g. M = 512 on 4096 -> 12288: 110 -> 108 us, M = 256: 72 -> 64 us):
-// the plane traffic grows with S, so 20 tiles (M = 256 on 5120^2) stay half
-// tiles at half the split count.  A layer too short to split takes the half
-// tiles whenever all of them fit one wave of workgroups.
-struct WideSplit {
-    uint32_t full, half;   // 256-column blocks of each width
-};
-constexpr uint32_t kWideSplitMinStages = 8;   // 64-channel stages per K split, at least
-static bool wide_can_split(const DeviceWeights& w) { return (w.input / 64) / kWideSplitMinStages >= 2; }
-static WideSplit wide_split(uint64_t m, const DeviceWeights& w) {
-    constexpr uint64_t kCus = 256;
-    const uint64_t mb = (m + 255) / 256, nc = w.output / 256, tiles = mb * nc;
-    if (2 * tiles <= kCus && (!wide_can_split(w) || 8 * tiles < kCus)) return {0, uint32_t(nc)};
-    return {uint32_t(nc), 0};
-}
-
-static bool gemm_wide(uint64_t m, const DeviceWeights& w) { return m >= 256 && w.output % 256 == 0; }
-
-// K split of a wide pass (no handoff) whose workgroups fill at most half of
-// the 256 CUs, e.g. M = 256..768 on 5120^2 (20 to 60 tiles): S workgroups per
-// tile, as many as one round holds, each over at least eight 64-channel
-// stages.  The planes add 2 S M N floats of traffic (written, then folded).
-// S depends on the layer and on the number of 256-row blocks, so rows of calls
-// in the same class share bits.
-static uint32_t wide_splits(uint64_t m, const DeviceWeights& w) {
-    if (!gemm_wide(m, w)) return 1;
-    const WideSplit sp = wide_split(m, w);
-    const uint64_t wgs = ((m + 255) / 256) * (uint64_t(sp.full) + 2 * uint64_t(sp.half));
-    if (2 * wgs > 256) return 1;
-    uint64_t s = 256 / wgs;
-    const uint64_t cap = (w.input / 64) / kWideSplitMinStages;
-    if (s > cap) s = cap;
-    return s > 1 ? uint32_t(s) : 1;
-}
-
-// K-split of the narrow (M < 256) kernel: N/128 column groups alone leave
-// most CUs idle (96 workgroups on 4096 -> 12288, 40 on 5120^2), so the input
-// splits in S power-of-two parts until the column groups x S reach the 256
-// CUs (S <= 16, whole 128-channel stages per split).  S depends on the layer
-// only, so every row of every M < 256 call has the same bits; it is part of
-// the core's accumulation order (planes folded in ascending split order from
-// +0, as the split GEMV does).
-static uint32_t narrow_splits(const DeviceWeights& w) {
-    const uint32_t groups = w.output / 128, stages = w.input / 128;
-    uint32_t s = 1;
-    while (groups * s < 256 && s < 16 && stages % (2 * s) == 0) s *= 2;
-    return s;
-}
-
-// K-split handoff of a wide pass with only 256 x 256 tiles: T = 256 q + x
-// tiles with 0 < x <= 128 (and T a multiple of the 8 XCDs) launch as x
-// heads, 256 q whole tiles and x tails (one workgroup per CU at a time), so
-// each CU runs about q + 1/2 tile-times instead of q + 1.
-struct Handoff {
-    uint32_t q = 0, x = 0;
-};
-static Handoff gemm_handoff(uint64_t m, const DeviceWeights& w) {
-    Handoff h;
-    if (!gemm_wide(m, w) || w.input / 64 < 2) return h;
-    const WideSplit sp = wide_split(m, w);
-    if (sp.half) return h;
-    const uint64_t tiles = ((m + 255) / 256) * (w.output / 256), rem = tiles % 256;
-    if (tiles < 256 || rem == 0 || rem > 128 || tiles % 8) return h;
-    h.q = uint32_t(tiles / 256);
-    h.x = uint32_t(rem);
-    return h;
-}
-static uint64_t handoff_bytes(uint32_t x) { return uint64_t(x) * 8 * 128 * 64 * sizeof(float); }
-
-// Workspace of one pass of m rows: fragment-order input, then the handoff's
-// partial accumulators and flags (wide) or the split planes (narrow).
-static uint64_t pass_workspace(const DeviceWeights& w, uint64_t m) {
-    if (!gemm_wide(m, w)) {
-        const uint32_t s = narrow_splits(w);
-        return afrag_bytes(w, m) + (s > 1 ? align256(uint64_t(s) * m * w.output * sizeof(float)) : 0);
-    }
-    const Handoff h = gemm_handoff(m, w);
-    const uint32_t s = wide_splits(m, w);
-    return afrag_bytes(w, m) + (h.x ? align256(handoff_bytes(h.x)) + align256(uint64_t(h.x) * 4) : 0) +
-           (s > 1 ? align256(uint64_t(s) * m * w.output * sizeof(float)) : 0);
-}
-
-uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows) {
-    const uint64_t pass = gemm_pass_rows(w);
-    if (rows <= pass) return pass_workspace(w, rows);
-    const uint64_t a = pass_workspace(w, pass), b = rows % pass ? pass_workspace(w, rows % pass) : 0;
-    return a > b ? a : b;
-}
-
-uint32_t gemm_launch_count(const DeviceWeights& w, uint64_t rows) {
-    const uint64_t pass = gemm_pass_rows(w);
-    uint32_t n = 0;
-    for (uint64_t r0 = 0; r0 < rows; r0 += pass) {
-        const uint64_t m = rows - r0 < pass ? rows - r0 : pass;
-        n += 2;
-        if (!gemm_wide(m, w) && narrow_splits(w) > 1) ++n;   // plane fold
-        if (gemm_wide(m, w)) {
-            const WideSplit sp = wide_split(m, w);
-            n += sp.full && sp.half;
-            if (wide_splits(m, w) > 1) ++n;   // plane fold
-        }
-    }
-    return n;
-}
-
-uint32_t gemm_split_count(const DeviceWeights& w, uint64_t rows) {
-    const uint64_t pass = gemm_pass_rows(w), m = rows < pass ? rows : pass;
-    return gemm_wide(m, w) ? wide_splits(m, w) : narrow_splits(w);
 }
 
 using GemmDispatch = hipError_t (*)(const GemmLaunch&);

@@ -1,46 +1,9 @@
-// Host side of the decode GEMV: decomposition, workspace, launches; plus the
-// finishing kernel and the diagnostic stage kernels.
+// Host side of the decode GEMV: launches (the split decomposition and
+// workspace sizes are in policy.cpp); plus the finishing kernels and the
+// diagnostic stage kernels.
 #include "gemv_kernel.hpp"
 
 namespace stx {
-
-// Split decomposition.  The whole matrix must be in flight at once for the
-// small decode shapes (8 MiB at K4 4096^2 is about one HBM latency-bandwidth
-// product), so aim for >= 512 workgroups of 4 waves (measured on MI355X:
-// 1024 adds more cross-workgroup fold traffic than it hides, 256 leaves SIMDs
-// idle); among candidate splits (bps = 8m with m dividing (I/16)/8, m <= 16)
-// take the largest bps that keeps the grid at or above that target, else the
-// smallest bps.
-GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t /*bits*/) {
-    const uint32_t nb = input / 16, nc = output / 128, units = nb / 8;
-    constexpr uint32_t target = 512;
-    // When no split count reaches the target (few column groups), 16-block
-    // splits are kept while they leave at least 128 workgroups: 8-block ones
-    // are dominated by each workgroup's fixed costs (4096 -> 1024 alone: 7.8
-    // -> 7.0 us; sixteen of them as the grouped o_a plan: 23.0 -> 20.4 us),
-    // while smaller layers (2048 -> 512) need the workgroups more.
-    GemvShape best = units % 2 == 0 && uint64_t(nc) * (nb / 16) >= 128 ? GemvShape{16, nb / 16}
-                                                                        : GemvShape{8, nb / 8};
-    for (uint32_t m = 1; m <= 16; ++m) {
-        if (units % m) continue;
-        const uint32_t bps = 8 * m, splits = nb / bps;
-        if (uint64_t(nc) * splits >= target) best = {bps, splits};
-    }
-    return best;
-}
-
-static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
-
-uint64_t gemv_workspace_bytes(const DeviceWeights& w, uint32_t rows) {
-    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
-    if (sh.splits <= 1) return 0;
-    return align256(uint64_t(sh.splits) * rows * w.output * sizeof(float));
-}
-
-uint64_t gemv_plane_words(const DeviceWeights& w, uint64_t rows) {
-    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
-    return sh.splits > 1 ? uint64_t(sh.splits) * rows * w.output : 0;
-}
 
 // Row template of a call: rows are computed in groups of 1, 2, 3, 4, 6 or 8
 // (the rows past the call's are zero inputs whose results are never stored).

@@ -1,24 +1,8 @@
-// Host side of the routed-expert block: split policy, workspace sizes, launches.
+// Host side of the routed-expert block: argument checks and launches (its
+// split policy and workspace sizes are in policy.cpp).
 #include "moe_kernel.hpp"
 
 namespace stx {
-
-MoeSplit moe_split(uint32_t input, uint32_t max_bps) {
-    const uint32_t blocks = input / 16;
-    uint32_t bps = 8;
-    for (uint32_t b = 16; b <= max_bps; b += 8)
-        if (blocks % b == 0) bps = b;
-    return {bps, blocks / bps};
-}
-
-uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H) {
-    return uint64_t(routes) * moe_split(I, MOE_GU_MAX_BPS).splits * 2 * H +
-           uint64_t(routes) * moe_split(H, MOE_D_MAX_BPS).splits * I;
-}
-
-uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H) {
-    return uint64_t(routes) * (H / 128) + uint64_t(rows) * (I / 128);
-}
 
 using MoeDispatch = hipError_t (*)(const MoeArgs&, hipStream_t);
 static const MoeDispatch gate_up_table[2] = {moe_gate_up_dispatch<2>, moe_gate_up_dispatch<3>};
