@@ -1,0 +1,560 @@
+// CPU contract test of the C ABI layer (api*.cpp, dispatch.cpp, policy.cpp
+// compiled unchanged against a fake HIP runtime).  It checks the status each
+// HIP failure maps to, that failed calls leave no device allocation behind,
+// that plan submission allocates, copies, synchronises and queries nothing,
+// and that every launcher receives device buffers large enough for its
+// policy.  The reference's own contract test follows the same idea with its
+// own fake (reference tests/test_api_contract.cpp:1-115, docs/API.md:349-374).
+#include "fake.hpp"
+#include "strix_trellis.h"
+#include "strix_trellis_amd.h"
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+static int checks = 0;
+#define CHECK(cond)                                                                    \
+    do {                                                                               \
+        ++checks;                                                                      \
+        if (!(cond)) {                                                                 \
+            std::fprintf(stderr, "%s:%d: CHECK failed: %s\n", __FILE__, __LINE__, #cond); \
+            std::exit(1);                                                              \
+        }                                                                              \
+    } while (0)
+#define STATUS(expr, want)                                                                           \
+    do {                                                                                             \
+        ++checks;                                                                                    \
+        const strix_status got_ = (expr);                                                            \
+        if (got_ != (want)) {                                                                        \
+            std::fprintf(stderr, "%s:%d: %s returned %d (%s), want %d\n", __FILE__, __LINE__, #expr, \
+                         int(got_), strix_status_string(got_), int(want));                          \
+            std::exit(1);                                                                            \
+        }                                                                                            \
+    } while (0)
+
+template <class T>
+static T header() {
+    T d;
+    std::memset(&d, 0, sizeof(d));
+    d.struct_size = sizeof(T);
+    d.abi_version = STRIX_TRELLIS_ABI_VERSION;
+    return d;
+}
+
+static strix_stream stream_of(hipStream_t s) {
+    strix_stream st = header<strix_stream>();
+    st.hip_stream = s;
+    return st;
+}
+
+// Host regions of one EXL3 linear (mul1 codebook), deterministic bytes.
+struct HostLinear {
+    uint64_t rows, columns;
+    uint32_t bits;
+    bool bias;
+    std::vector<uint8_t> trellis, suh, svh, b;
+    HostLinear(uint64_t n, uint64_t i, uint32_t k, bool with_bias) : rows(n), columns(i), bits(k), bias(with_bias) {
+        trellis.resize(n * i / 8 * k);
+        suh.resize(i * 2);
+        svh.resize(n * 2);
+        if (bias) b.resize(n * 4);
+        uint32_t x = 12345;
+        for (auto* v : {&trellis, &suh, &svh, &b})
+            for (auto& c : *v) c = uint8_t((x = x * 1103515245u + 12345u) >> 16);
+    }
+    strix_exl3_parts_desc parts() const {
+        strix_exl3_parts_desc d = header<strix_exl3_parts_desc>();
+        d.transport_version = STRIX_TRELLIS_TRANSPORT_VERSION;
+        d.bits_x2 = bits * 2;
+        d.rows = rows;
+        d.columns = columns;
+        d.codebook = STRIX_CODEBOOK_MUL1;
+        d.marker = STRIX_EXL3_MARKER_MUL1;
+        d.trellis = {trellis.data(), trellis.size()};
+        d.suh = {suh.data(), suh.size()};
+        d.svh = {svh.data(), svh.size()};
+        if (bias) d.bias = {b.data(), b.size()};
+        return d;
+    }
+};
+
+static void* device_alloc(size_t bytes) {
+    void* p = nullptr;
+    CHECK(hipMalloc(&p, bytes) == hipSuccess);
+    return p;
+}
+
+static strix_tensor_desc tensor(void* data, uint64_t bytes, uint64_t rows, uint64_t width, uint32_t rank) {
+    strix_tensor_desc t = header<strix_tensor_desc>();
+    t.data = data;
+    t.buffer_bytes = bytes;
+    t.dtype = STRIX_DTYPE_F32;
+    t.rank = rank;
+    if (rank == 1) {
+        t.shape[0] = width;
+        t.strides[0] = 1;
+    } else {
+        t.shape[0] = rows;
+        t.shape[1] = width;
+        t.strides[0] = width;
+        t.strides[1] = 1;
+    }
+    return t;
+}
+
+// No HIP call beyond the device query that validates the calling thread.
+static void check_quiet_since(const fake::Counters& before) {
+    CHECK(fake::n.mallocs == before.mallocs);
+    CHECK(fake::n.frees == before.frees);
+    CHECK(fake::n.copies == before.copies);
+    CHECK(fake::n.syncs == before.syncs);
+    CHECK(fake::n.pointer_queries == before.pointer_queries);
+    CHECK(fake::n.range_queries == before.range_queries);
+    CHECK(fake::n.stream_queries == before.stream_queries);
+}
+
+static void context_rules() {
+    strix_context_desc cd = header<strix_context_desc>();
+    strix_context c = reinterpret_cast<strix_context>(0x1);
+    STATUS(strix_context_create(&cd, &c), STRIX_SUCCESS);
+    CHECK(c != nullptr);
+    STATUS(strix_context_destroy(c), STRIX_SUCCESS);
+
+    // Only gfx950 with 64-lane waves is accepted.
+    const char* wrong[] = {"gfx1151", "gfx942:sramecc+:xnack-", "gfx9500", "gfx95"};
+    for (const char* a : wrong) {
+        fake::arch = a;
+        c = reinterpret_cast<strix_context>(0x1);
+        STATUS(strix_context_create(&cd, &c), STRIX_ERROR_UNSUPPORTED_DEVICE);
+        CHECK(c == nullptr);
+    }
+    fake::arch = "gfx950";
+    STATUS(strix_context_create(&cd, &c), STRIX_SUCCESS);
+    STATUS(strix_context_destroy(c), STRIX_SUCCESS);
+    fake::arch = "gfx950:sramecc+:xnack-";
+    fake::wave = 32;
+    STATUS(strix_context_create(&cd, &c), STRIX_ERROR_UNSUPPORTED_DEVICE);
+    fake::wave = 64;
+
+    // Device property failures.
+    const struct {
+        hipError_t e;
+        strix_status s;
+    } props[] = {{hipErrorNoDevice, STRIX_ERROR_UNSUPPORTED_DEVICE},
+                 {hipErrorInvalidDevice, STRIX_ERROR_UNSUPPORTED_DEVICE},
+                 {hipErrorOutOfMemory, STRIX_ERROR_OUT_OF_MEMORY},
+                 {hipErrorUnknown, STRIX_ERROR_BACKEND}};
+    for (const auto& p : props) {
+        fake::props_error = p.e;
+        c = reinterpret_cast<strix_context>(0x1);
+        STATUS(strix_context_create(&cd, &c), p.s);
+        CHECK(c == nullptr);
+    }
+    fake::props_error = hipSuccess;
+    cd.device_ordinal = 9;
+    STATUS(strix_context_create(&cd, &c), STRIX_ERROR_UNSUPPORTED_DEVICE);
+    cd.device_ordinal = -1;
+    STATUS(strix_context_create(&cd, &c), STRIX_ERROR_INVALID_ARGUMENT);
+    cd.device_ordinal = 0;
+
+    // Descriptor header rules.
+    cd.struct_size = sizeof(cd) - 8;
+    STATUS(strix_context_create(&cd, &c), STRIX_ERROR_ABI_MISMATCH);
+    cd.struct_size = sizeof(cd);
+    cd.abi_version = 2;
+    STATUS(strix_context_create(&cd, &c), STRIX_ERROR_ABI_MISMATCH);
+    cd.abi_version = STRIX_TRELLIS_ABI_VERSION;
+    cd.reserved[3] = 1;
+    STATUS(strix_context_create(&cd, &c), STRIX_ERROR_INVALID_ARGUMENT);
+    cd.reserved[3] = 0;
+    cd.flags = 1;
+    STATUS(strix_context_create(&cd, &c), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_context_create(nullptr, &c), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_context_create(&cd, nullptr), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_context_destroy(nullptr), STRIX_ERROR_INVALID_ARGUMENT);
+}
+
+// Every prepare failure drains the stream, frees its allocation and returns
+// the mapped status.
+static void prepare_failures(strix_context c, hipStream_t hs) {
+    const HostLinear L(256, 512, 4, true);
+    const strix_exl3_parts_desc parts = L.parts();
+    strix_stream st = stream_of(hs);
+    const size_t live0 = fake::live.size();
+    strix_weights w = reinterpret_cast<strix_weights>(0x1);
+
+    fake::malloc_fail_at = 0;
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_ERROR_OUT_OF_MEMORY);
+    CHECK(w == nullptr && fake::live.size() == live0);
+    fake::malloc_fail_at = 0;
+    fake::malloc_error = hipErrorUnknown;
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_ERROR_BACKEND);
+    fake::reset_failures();
+
+    for (int at = 0; at < 4; ++at) {   // trellis, suh, svh, bias copies
+        const fake::Counters before = fake::n;
+        fake::copy_fail_at = at;
+        STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_ERROR_BACKEND);
+        CHECK(w == nullptr && fake::live.size() == live0);
+        CHECK(fake::n.copies == before.copies + at + 1);   // nothing enqueued after the failure
+        CHECK(fake::n.syncs == before.syncs + 1);          // the stream is drained before the free
+        fake::reset_failures();
+    }
+    fake::copy_fail_at = 1;
+    fake::copy_error = hipErrorOutOfMemory;
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_ERROR_OUT_OF_MEMORY);
+    fake::reset_failures();
+    fake::sync_fail_at = 0;
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_ERROR_BACKEND);
+    CHECK(w == nullptr && fake::live.size() == live0);
+    fake::reset_failures();
+
+    // Thread and stream validation happens before any allocation.
+    fake::get_device_error = hipErrorUnknown;
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_ERROR_BACKEND);
+    fake::get_device_error = hipSuccess;
+    fake::current_device = 1;
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_ERROR_INVALID_ARGUMENT);
+    fake::current_device = 0;
+    strix_stream other = stream_of(fake::make_stream(1));
+    STATUS(strix_weights_prepare_parts(c, &parts, &other, &w), STRIX_ERROR_INVALID_ARGUMENT);
+    strix_stream bogus = stream_of(reinterpret_cast<hipStream_t>(&other));
+    STATUS(strix_weights_prepare_parts(c, &parts, &bogus, &w), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_weights_prepare_parts(c, &parts, nullptr, &w), STRIX_ERROR_INVALID_ARGUMENT);
+    CHECK(fake::live.size() == live0);
+
+    // Format rules reject before allocating.
+    strix_exl3_parts_desc bad = parts;
+    bad.marker = STRIX_EXL3_MARKER_MCG;
+    STATUS(strix_weights_prepare_parts(c, &bad, &st, &w), STRIX_ERROR_UNSUPPORTED_FORMAT);
+    bad = parts;
+    bad.columns = 500;
+    STATUS(strix_weights_prepare_parts(c, &bad, &st, &w), STRIX_ERROR_UNSUPPORTED_FORMAT);
+    bad = parts;
+    bad.trellis.bytes -= 4;
+    STATUS(strix_weights_prepare_parts(c, &bad, &st, &w), STRIX_ERROR_UNSUPPORTED_FORMAT);
+    bad = parts;
+    bad.svh.data = bad.suh.data;   // overlapping host regions
+    STATUS(strix_weights_prepare_parts(c, &bad, &st, &w), STRIX_ERROR_INVALID_ARGUMENT);
+    bad = parts;
+    bad.bits_x2 = 7;
+    STATUS(strix_weights_prepare_parts(c, &bad, &st, &w), STRIX_ERROR_UNSUPPORTED_FORMAT);
+    CHECK(fake::live.size() == live0);
+
+    // Success: one allocation, one copy per region, one synchronisation, and
+    // the regions land in 256-byte aligned slices in order.
+    const fake::Counters before = fake::n;
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_SUCCESS);
+    CHECK(fake::n.mallocs == before.mallocs + 1 && fake::n.copies == before.copies + 4 &&
+          fake::n.syncs == before.syncs + 1);
+    const void* span = nullptr;
+    uint64_t span_bytes = 0;
+    STATUS(strix_weights_device_span(w, &span, &span_bytes), STRIX_SUCCESS);
+    CHECK(fake::in_live_block(span, span_bytes));
+    const uint8_t* base = static_cast<const uint8_t*>(span);
+    uint64_t off = 0;
+    for (const auto* v : {&L.trellis, &L.suh, &L.svh, &L.b}) {
+        off = (off + 255) / 256 * 256;
+        CHECK(std::memcmp(base + off, v->data(), v->size()) == 0);
+        off += v->size();
+    }
+    CHECK(span_bytes == off);
+    STATUS(strix_context_destroy(c), STRIX_ERROR_INVALID_ARGUMENT);   // weights still live
+    fake::free_fail_at = 0;
+    STATUS(strix_weights_destroy(w), STRIX_ERROR_BACKEND);            // a failed free keeps the handle
+    STATUS(strix_weights_destroy(w), STRIX_SUCCESS);
+    CHECK(fake::live.size() == live0);
+}
+
+struct Dense {
+    HostLinear host;
+    strix_weights w = nullptr;
+    void *x = nullptr, *y = nullptr, *ws = nullptr;
+    uint64_t rows = 0, ws_bytes = 0;
+};
+
+static strix_matmul_desc matmul(const Dense& d, uint64_t rows, uint32_t rank) {
+    strix_matmul_desc m = header<strix_matmul_desc>();
+    m.weights = d.w;
+    m.input = tensor(d.x, rows * d.host.columns * 4, rows, d.host.columns, rank);
+    m.output = tensor(d.y, rows * d.host.rows * 4, rows, d.host.rows, rank);
+    m.alpha = 0.5f;
+    m.beta = 0.25f;
+    m.workspace = d.ws;
+    m.workspace_bytes = d.ws_bytes;
+    return m;
+}
+
+static void direct_calls(strix_context c, hipStream_t hs) {
+    Dense d{HostLinear(1024, 2048, 4, false)};
+    d.rows = 64;
+    strix_stream st = stream_of(hs);
+    const strix_exl3_parts_desc parts = d.host.parts();
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &d.w), STRIX_SUCCESS);
+    d.x = device_alloc(d.rows * d.host.columns * 4);
+    d.y = device_alloc(d.rows * d.host.rows * 4);
+    strix_matmul_desc m = matmul(d, d.rows, 2);
+    STATUS(strix_matmul_workspace_bytes(c, &m, &d.ws_bytes), STRIX_SUCCESS);
+    CHECK(d.ws_bytes > 0 && d.ws_bytes % 256 == 0);
+    d.ws = device_alloc(d.ws_bytes);
+    const size_t live0 = fake::live.size();
+
+    // GEMM: one launcher call with the caller's workspace, scalars forwarded.
+    m = matmul(d, d.rows, 2);
+    fake::launches.clear();
+    STATUS(strix_gemm(c, &m, &st), STRIX_SUCCESS);
+    CHECK(fake::launches.size() == 1 && fake::launches[0].name == "gemm" && fake::launches[0].rows == d.rows);
+    CHECK(fake::launches[0].workspace == d.ws && fake::launches[0].stream == hs);
+    CHECK(fake::launches[0].alpha == 0.5f && fake::launches[0].beta == 0.25f);
+
+    // GEMV of 1..8 rows and of a rank-1 vector.
+    for (uint64_t r : {1u, 3u, 8u}) {
+        m = matmul(d, r, 2);
+        fake::launches.clear();
+        STATUS(strix_gemv(c, &m, &st), STRIX_SUCCESS);
+        CHECK(fake::launches.size() == 1 && fake::launches[0].name == "gemv" && fake::launches[0].rows == r);
+    }
+    m = matmul(d, 1, 1);
+    fake::launches.clear();
+    STATUS(strix_gemv(c, &m, &st), STRIX_SUCCESS);
+    CHECK(fake::launches.size() == 1 && fake::launches[0].rows == 1);
+    m = matmul(d, 9, 2);
+    STATUS(strix_gemv(c, &m, &st), STRIX_ERROR_UNSUPPORTED_FORMAT);
+
+    // Zero rows: success without a launch.
+    m = matmul(d, 0, 2);
+    fake::launches.clear();
+    STATUS(strix_gemm(c, &m, &st), STRIX_SUCCESS);
+    CHECK(fake::launches.empty());
+
+    // Launch failures map to BACKEND / OUT_OF_MEMORY.
+    m = matmul(d, d.rows, 2);
+    fake::launch_fail_at = 0;
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_BACKEND);
+    fake::launch_fail_at = 0;
+    fake::launch_error = hipErrorOutOfMemory;
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_OUT_OF_MEMORY);
+    fake::reset_failures();
+
+    // Storage rules: host memory, short allocations, short workspaces.
+    std::vector<float> host_x(d.rows * d.host.columns);
+    fake::launches.clear();
+    m = matmul(d, d.rows, 2);
+    m.input.data = host_x.data();
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    void* short_y = device_alloc(d.rows * d.host.rows * 4 - 256);
+    m = matmul(d, d.rows, 2);
+    m.output.data = short_y;   // buffer_bytes claims more than the allocation holds
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_INSUFFICIENT_BUFFER);
+    m = matmul(d, d.rows, 2);
+    m.workspace_bytes -= 256;
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_INSUFFICIENT_BUFFER);
+    m = matmul(d, d.rows, 2);
+    m.workspace = static_cast<char*>(d.ws) + 16;   // misaligned
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    m = matmul(d, d.rows, 2);
+    m.output.data = d.x;   // output aliases input
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    m = matmul(d, d.rows, 2);
+    m.input.data = const_cast<void*>(static_cast<const void*>(parts.trellis.data));
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    CHECK(fake::launches.empty());
+    fake::current_device = 1;
+    m = matmul(d, d.rows, 2);
+    STATUS(strix_gemm(c, &m, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    fake::current_device = 0;
+    CHECK(hipFree(short_y) == hipSuccess);
+    CHECK(fake::live.size() == live0);
+
+    // Linear plans: create validates and owns its planes; submit is quiet.
+    uint32_t bps = 0, splits = 0;
+    STATUS(strix_amd_gemv_shape(d.w, &bps, &splits), STRIX_SUCCESS);
+    CHECK(splits > 1);   // this geometry has split-K partial planes
+    m = matmul(d, 4, 2);
+    const fake::Counters at_create = fake::n;
+    strix_linear_plan gp = nullptr;
+    STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &gp), STRIX_SUCCESS);
+    CHECK(fake::n.mallocs == at_create.mallocs + 1 && fake::n.syncs == at_create.syncs + 1);
+    CHECK(fake::live.size() == live0 + 1);
+    uint32_t planned = 0;
+    STATUS(strix_amd_plan_launches(gp, &planned), STRIX_SUCCESS);
+    CHECK(planned == 1);
+    for (int rep = 0; rep < 3; ++rep) {
+        fake::launches.clear();
+        const fake::Counters before = fake::n;
+        STATUS(strix_linear_plan_submit(gp), STRIX_SUCCESS);
+        check_quiet_since(before);
+        CHECK(fake::launches.size() == 1 && fake::launches[0].name == "gemv_fused");
+        CHECK(fake::launches[0].rows == 4 && fake::launches[0].stream == hs && fake::launches[0].planes);
+    }
+    fake::launch_fail_at = 0;
+    STATUS(strix_linear_plan_submit(gp), STRIX_ERROR_BACKEND);
+    fake::reset_failures();
+
+    strix_linear_plan mp = nullptr;
+    m = matmul(d, d.rows, 2);
+    STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMM, &mp), STRIX_SUCCESS);
+    fake::launches.clear();
+    const fake::Counters before = fake::n;
+    STATUS(strix_linear_plan_submit(mp), STRIX_SUCCESS);
+    check_quiet_since(before);
+    CHECK(fake::launches.size() == 1 && fake::launches[0].name == "gemm" && fake::launches[0].workspace == d.ws);
+
+    // Plan creation failures free the planes they allocated.
+    m = matmul(d, 2, 2);
+    const size_t live1 = fake::live.size();
+    strix_linear_plan bad = reinterpret_cast<strix_linear_plan>(0x1);
+    fake::malloc_fail_at = 0;
+    STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &bad), STRIX_ERROR_OUT_OF_MEMORY);
+    CHECK(bad == nullptr && fake::live.size() == live1);
+    fake::reset_failures();
+    fake::launch_fail_at = 0;   // the EMPTY fill
+    STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &bad), STRIX_ERROR_BACKEND);
+    CHECK(bad == nullptr && fake::live.size() == live1);
+    fake::reset_failures();
+    fake::sync_fail_at = 0;
+    STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &bad), STRIX_ERROR_BACKEND);
+    CHECK(bad == nullptr && fake::live.size() == live1);
+    fake::reset_failures();
+    STATUS(strix_linear_plan_create(c, &m, &st, 7, &bad), STRIX_ERROR_INVALID_ARGUMENT);
+
+    // Weights outlive their plans; the planes go with the weights.
+    STATUS(strix_weights_destroy(d.w), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_linear_plan_destroy(gp), STRIX_SUCCESS);
+    STATUS(strix_weights_destroy(d.w), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_linear_plan_destroy(mp), STRIX_SUCCESS);
+    STATUS(strix_weights_destroy(d.w), STRIX_SUCCESS);
+    CHECK(fake::live.size() == live0 - 1);
+    for (void* p : {d.x, d.y, d.ws}) CHECK(hipFree(p) == hipSuccess);
+}
+
+// Routed-expert plan over host routes: creation failures leave nothing
+// behind, submission is quiet, and invalid routes are rejected up front.
+static void moe_plan(strix_context c, hipStream_t hs) {
+    const uint32_t I = 256, H = 512, rows = 2, k = 2, experts = 3;
+    strix_stream st = stream_of(hs);
+    std::vector<HostLinear> host;
+    for (uint32_t e = 0; e < experts; ++e) {
+        host.emplace_back(H, I, 2, false);
+        host.emplace_back(H, I, 2, false);
+        host.emplace_back(I, H, 3, false);
+    }
+    std::vector<strix_weights> ws(host.size());
+    for (size_t i = 0; i < host.size(); ++i) {
+        const strix_exl3_parts_desc p = host[i].parts();
+        STATUS(strix_weights_prepare_parts(c, &p, &st, &ws[i]), STRIX_SUCCESS);
+    }
+    std::vector<strix_tp_expert_desc> ex(experts);
+    for (uint32_t e = 0; e < experts; ++e) {
+        ex[e] = header<strix_tp_expert_desc>();
+        ex[e].expert_id = 10 + e;
+        ex[e].gate = ws[3 * e];
+        ex[e].up = ws[3 * e + 1];
+        ex[e].down = ws[3 * e + 2];
+    }
+    void* x = device_alloc(rows * I * 4);
+    void* y = device_alloc(rows * I * 4);
+    uint32_t ids[rows * k] = {10, 12, 12, 11};
+    float scores[rows * k] = {0.75f, 0.25f, 1.0f, 0.0f};
+    strix_tp_moe_desc d;
+    strix_tp_moe_desc_init(&d);
+    d.input = tensor(x, rows * I * 4, rows, I, 2);
+    d.output = tensor(y, rows * I * 4, rows, I, 2);
+    d.experts = ex.data();
+    d.expert_count = experts;
+    d.route_ids = ids;
+    d.route_ids_count = rows * k;
+    d.route_scores = scores;
+    d.route_scores_count = rows * k;
+    d.alpha = 1.0f;
+    uint64_t need = 0;
+    STATUS(strix_tp_moe_workspace_bytes(c, &d, &need), STRIX_SUCCESS);
+    CHECK(need >= uint64_t(rows) * k * H * 4);
+    d.workspace = device_alloc(need);
+    d.workspace_bytes = need;
+    const size_t live0 = fake::live.size();
+
+    strix_tp_moe_plan p = reinterpret_cast<strix_tp_moe_plan>(0x1);
+    fake::malloc_fail_at = 0;
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_OUT_OF_MEMORY);
+    CHECK(p == nullptr && fake::live.size() == live0);
+    fake::reset_failures();
+    for (int at = 0; at < 3; ++at) {   // expert table, route ids, route scores
+        fake::copy_fail_at = at;
+        STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_BACKEND);
+        CHECK(p == nullptr && fake::live.size() == live0);
+        fake::reset_failures();
+    }
+    fake::launch_fail_at = 0;   // the counter fill
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_BACKEND);
+    CHECK(p == nullptr && fake::live.size() == live0);
+    fake::reset_failures();
+    fake::sync_fail_at = 0;
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_BACKEND);
+    CHECK(p == nullptr && fake::live.size() == live0);
+    fake::reset_failures();
+
+    // Route rules.
+    ids[1] = 99;   // unknown expert id
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+    ids[1] = 10;   // repeated within a row
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+    ids[1] = 12;
+    scores[0] = -1.0f;
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+    scores[0] = 0.75f;
+    d.workspace_bytes = need - 4;
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_ERROR_INSUFFICIENT_BUFFER);
+    d.workspace_bytes = need;
+    CHECK(fake::live.size() == live0);
+
+    STATUS(strix_tp_moe_plan_create(c, &d, &st, &p), STRIX_SUCCESS);
+    CHECK(fake::live.size() == live0 + 1);
+    STATUS(strix_weights_destroy(ws[0]), STRIX_ERROR_INVALID_ARGUMENT);   // retained by the plan
+    for (int rep = 0; rep < 2; ++rep) {
+        fake::launches.clear();
+        const fake::Counters before = fake::n;
+        STATUS(strix_tp_moe_plan_submit(p), STRIX_SUCCESS);
+        check_quiet_since(before);
+        CHECK(fake::launches.size() == 2 && fake::launches[0].name == "moe_gate_up" &&
+              fake::launches[1].name == "moe_down");
+    }
+    fake::launches.clear();
+    STATUS(strix_tp_moe_plan_gate_up(p), STRIX_SUCCESS);
+    STATUS(strix_tp_moe_plan_down(p), STRIX_SUCCESS);
+    CHECK(fake::launches.size() == 2);
+    fake::launch_fail_at = 1;   // the down launch
+    STATUS(strix_tp_moe_plan_submit(p), STRIX_ERROR_BACKEND);
+    fake::reset_failures();
+    STATUS(strix_tp_moe_plan_destroy(p), STRIX_SUCCESS);
+    CHECK(fake::live.size() == live0);
+    for (strix_weights w : ws) STATUS(strix_weights_destroy(w), STRIX_SUCCESS);
+    for (void* q : {x, y, d.workspace}) CHECK(hipFree(q) == hipSuccess);
+}
+
+int main() {
+    context_rules();
+    strix_context_desc cd = header<strix_context_desc>();
+    strix_context c = nullptr;
+    STATUS(strix_context_create(&cd, &c), STRIX_SUCCESS);
+    const hipStream_t hs = fake::make_stream(0);
+    prepare_failures(c, hs);
+    direct_calls(c, hs);
+    moe_plan(c, hs);
+    // The default stream (NULL) is accepted everywhere a stream is.
+    {
+        const HostLinear L(128, 128, 2, false);
+        const strix_exl3_parts_desc parts = L.parts();
+        strix_stream st = stream_of(nullptr);
+        strix_weights w = nullptr;
+        STATUS(strix_weights_prepare_parts(c, &parts, &st, &w), STRIX_SUCCESS);
+        STATUS(strix_weights_destroy(w), STRIX_SUCCESS);
+    }
+    STATUS(strix_context_destroy(c), STRIX_SUCCESS);
+    CHECK(fake::live.empty());
+    fake::destroy_streams();
+    std::printf("contract: %d checks passed\n", checks);
+    return 0;
+}

@@ -1,0 +1,179 @@
+// Fake kernel launchers.  Each records its call, checks that every device
+// buffer the real kernels would touch lies inside a live fake allocation of
+// sufficient size (and, for the single-launch GEMV, that its partial planes
+// arrive EMPTY-filled), and returns the injected launch result.  A failed
+// check aborts: it is a contract violation of the API layer.
+#include "fake.hpp"
+#include "backend.hpp"
+#include "moe.hpp"
+
+#include <cstdio>
+#include <cstdlib>
+
+namespace {
+
+void require(bool ok, const char* what, const char* launcher) {
+    if (ok) return;
+    std::fprintf(stderr, "contract violation in %s: %s\n", launcher, what);
+    std::abort();
+}
+
+fake::Launch record(const char* name, uint64_t rows, const void* ws, const void* planes, hipStream_t s, float alpha,
+                    float beta) {
+    fake::Launch l;
+    l.name = name;
+    l.rows = rows;
+    l.workspace = ws;
+    l.planes = planes;
+    l.stream = s;
+    l.alpha = alpha;
+    l.beta = beta;
+    fake::launches.push_back(l);
+    return l;
+}
+
+// The input and output rows of a linear call lie in device memory.
+void check_call(const stx::DeviceWeights& w, const stx::LinearCall& c, const char* who) {
+    require(c.rows > 0, "zero rows reach a launcher", who);
+    const uint64_t xb = ((c.rows - 1) * c.x_row_stride + w.input) * 4;
+    const uint64_t yb = ((c.rows - 1) * c.y_row_stride + w.output) * 4;
+    require(fake::in_live_block(c.x, xb), "input outside device memory", who);
+    require(fake::in_live_block(c.y, yb), "output outside device memory", who);
+    require(fake::in_live_block(w.trellis, w.trellis_bytes), "trellis outside device memory", who);
+}
+
+}  // namespace
+
+namespace stx {
+
+hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& c, hipStream_t s) {
+    check_call(w, c, "launch_gemv");
+    const uint64_t need = gemv_workspace_bytes(w, uint32_t(c.rows));
+    require(!need || fake::in_live_block(c.workspace, need), "GEMV workspace too small", "launch_gemv");
+    record("gemv", c.rows, c.workspace, nullptr, s, c.alpha, c.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& c, float* planes, hipStream_t s) {
+    check_call(w, c, "launch_gemv_fused");
+    const uint64_t words = gemv_plane_words(w, c.rows);
+    require(fake::in_live_block(planes, words * 4), "partial planes outside device memory", "launch_gemv_fused");
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(planes);
+    for (uint64_t i = 0; i < words; ++i) require(p[i] == GEMV_PLANE_EMPTY, "planes not EMPTY on entry", "launch_gemv_fused");
+    record("gemv_fused", c.rows, c.workspace, planes, s, c.alpha, c.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& c, const float* planes, uint32_t splits,
+                               hipStream_t s) {
+    check_call(w, c, "launch_plane_finish");
+    require(fake::in_live_block(planes, uint64_t(splits) * c.rows * w.output * 4), "planes outside device memory",
+            "launch_plane_finish");
+    record("plane_finish", c.rows, c.workspace, planes, s, c.alpha, c.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_gemv_grouped(const DeviceWeights& g, const GroupWeights* table, uint32_t groups,
+                               const LinearCall& c, uint64_t x_group_stride, uint64_t y_group_stride,
+                               bool single_launch, hipStream_t s) {
+    require(groups > 0, "no groups", "launch_gemv_grouped");
+    require(fake::in_live_block(table, groups * sizeof(GroupWeights)), "group table outside device memory",
+            "launch_gemv_grouped");
+    const uint64_t xb = ((groups - 1) * x_group_stride + (c.rows - 1) * c.x_row_stride + g.input) * 4;
+    const uint64_t yb = ((groups - 1) * y_group_stride + (c.rows - 1) * c.y_row_stride + g.output) * 4;
+    require(fake::in_live_block(c.x, xb), "grouped input outside device memory", "launch_gemv_grouped");
+    require(fake::in_live_block(c.y, yb), "grouped output outside device memory", "launch_gemv_grouped");
+    if (single_launch) {
+        const uint64_t words = uint64_t(groups) * gemv_plane_words(g, c.rows);
+        require(fake::in_live_block(c.workspace, words * 4), "grouped planes outside device memory",
+                "launch_gemv_grouped");
+        const uint32_t* p = static_cast<const uint32_t*>(c.workspace);
+        for (uint64_t i = 0; i < words; ++i)
+            require(p[i] == GEMV_PLANE_EMPTY, "grouped planes not EMPTY on entry", "launch_gemv_grouped");
+    }
+    record(single_launch ? "gemv_grouped_fused" : "gemv_grouped", c.rows, c.workspace, nullptr, s, c.alpha, c.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& c, hipStream_t s) {
+    check_call(w, c, "launch_gemm");
+    require(fake::in_live_block(c.workspace, gemm_workspace_bytes(w, c.rows)), "GEMM workspace too small",
+            "launch_gemm");
+    record("gemm", c.rows, c.workspace, nullptr, s, c.alpha, c.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_decode(const DeviceWeights& w, _Float16* q, hipStream_t s) {
+    require(fake::in_live_block(q, uint64_t(w.input) * w.output * 2), "decode output outside device memory",
+            "launch_decode");
+    record("decode", 0, nullptr, nullptr, s, 0, 0);
+    return fake::launch_result();
+}
+
+hipError_t launch_input_stage(const DeviceWeights& w, const float* x, uint64_t rows, _Float16* a, hipStream_t s) {
+    require(fake::in_live_block(x, rows * w.input * 4), "stage input outside device memory", "launch_input_stage");
+    require(fake::in_live_block(a, rows * w.input * 2), "stage output outside device memory", "launch_input_stage");
+    record("input_stage", rows, nullptr, nullptr, s, 0, 0);
+    return fake::launch_result();
+}
+
+hipError_t launch_output_stage(const DeviceWeights& w, const float* core, uint64_t rows, float* y, float alpha,
+                               float beta, hipStream_t s) {
+    require(fake::in_live_block(core, rows * w.output * 4), "core outside device memory", "launch_output_stage");
+    require(fake::in_live_block(y, rows * w.output * 4), "output outside device memory", "launch_output_stage");
+    record("output_stage", rows, nullptr, nullptr, s, alpha, beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStream_t s) {
+    require(fake::in_live_block(p, count * 4), "fill outside device memory", "launch_fill_u32");
+    record("fill", count, nullptr, p, s, 0, 0);
+    const hipError_t e = fake::launch_result();
+    if (e == hipSuccess)
+        for (uint64_t i = 0; i < count; ++i) p[i] = value;
+    return e;
+}
+
+static void check_moe(const MoeArgs& a, bool gate_up, const char* who) {
+    const uint64_t routes = uint64_t(a.rows) * a.topk;
+    require(fake::in_live_block(a.bank, a.bank_count * sizeof(MoeExpert)), "expert table outside device memory", who);
+    require(fake::in_live_block(a.ids, routes * 4), "route ids outside device memory", who);
+    require(fake::in_live_block(a.scores, routes * 4), "route scores outside device memory", who);
+    require(fake::in_live_block(a.hidden, routes * a.H * 4), "hidden outside device memory", who);
+    if (gate_up) {
+        require(fake::in_live_block(a.x, ((a.rows - 1) * a.x_stride + a.I) * 4), "input outside device memory", who);
+        const uint64_t words = routes * (a.H / 128);
+        require(fake::in_live_block(a.c_gu, words * 4), "gate/up counters outside device memory", who);
+        for (uint64_t i = 0; i < words; ++i) require(a.c_gu[i] == 0, "gate/up counters not zero on entry", who);
+        require(fake::in_live_block(a.p_gu, routes * a.s_gu * 2 * a.H * 4), "gate/up planes outside device memory",
+                who);
+    } else {
+        require(fake::in_live_block(a.y, ((a.rows - 1) * a.y_stride + a.I) * 4), "output outside device memory", who);
+        const uint64_t words = uint64_t(a.rows) * (a.I / 128);
+        require(fake::in_live_block(a.c_d, words * 4), "down counters outside device memory", who);
+        for (uint64_t i = 0; i < words; ++i) require(a.c_d[i] == 0, "down counters not zero on entry", who);
+        require(fake::in_live_block(a.p_d, routes * a.s_d * a.I * 4), "down planes outside device memory", who);
+    }
+}
+
+hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t s) {
+    check_moe(a, true, "launch_moe_gate_up");
+    record("moe_gate_up", a.rows, nullptr, nullptr, s, a.alpha, a.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_moe_down(const MoeArgs& a, hipStream_t s) {
+    check_moe(a, false, "launch_moe_down");
+    record("moe_down", a.rows, nullptr, nullptr, s, a.alpha, a.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_moe_swiglu(const float* g, const float* u, float* h, uint64_t count, hipStream_t s) {
+    require(fake::in_live_block(g, count * 4) && fake::in_live_block(u, count * 4) &&
+                fake::in_live_block(h, count * 4),
+            "SwiGLU operands outside device memory", "launch_moe_swiglu");
+    record("moe_swiglu", count, nullptr, nullptr, s, 0, 0);
+    return fake::launch_result();
+}
+
+}  // namespace stx
