@@ -16,7 +16,7 @@ Parity pinning (tests/test_oracle_codec.py):
                      and ``struct '<e'`` rounding, plus the 8-state bit vectors
                      of tests/test_reference.py:83-95;
   * permutation   -- the explicit first/last eight coordinates of
-                     docs/DESIGN.md:106-109 and the lane/fragment formula of
+                     reference docs/DESIGN.md:106-109 and the lane/fragment formula of
                      tests/test_reference.py:69-81 over all 256 positions.
 """
 from functools import lru_cache
@@ -107,7 +107,7 @@ def unpack_states_serial(tile_words, k):
     """One tile, bit-serial: a 16-bit shift register fed MSB-first ring bits.
 
     Independent of ``unpack_states``: it starts from the last 16 ring bits
-    (the wrap of docs/DESIGN.md:78-83) and shifts in ``width`` bits per state.
+    (the wrap of reference docs/DESIGN.md:78-83) and shifts in ``width`` bits per state.
     """
     words, need = _as_u16_words(tile_words, k)
     if words.ndim != 1:

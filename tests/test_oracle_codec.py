@@ -92,7 +92,7 @@ def test_fragment_coordinates_all_positions():
 
 
 def test_first_and_last_eight_coordinates():
-    # docs/DESIGN.md:106-109: explicit coordinates of positions 0..7 and 248..255.
+    # reference docs/DESIGN.md:106-109: explicit coordinates of positions 0..7 and 248..255.
     first = [(0, 0), (1, 0), (8, 0), (9, 0), (0, 8), (1, 8), (8, 8), (9, 8)]
     last = [(6, 7), (7, 7), (14, 7), (15, 7), (6, 15), (7, 15), (14, 15), (15, 15)]
     for pos, (r, c) in enumerate(first):
