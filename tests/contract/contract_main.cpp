@@ -6,6 +6,7 @@
 // policy.  The reference's own contract test follows the same idea with its
 // own fake (reference tests/test_api_contract.cpp:1-115, docs/API.md:349-374).
 #include "fake.hpp"
+#include "policy.hpp"
 #include "strix_trellis.h"
 #include "strix_trellis_amd.h"
 
@@ -534,7 +535,76 @@ static void moe_plan(strix_context c, hipStream_t hs) {
     for (void* q : {x, y, d.workspace}) CHECK(hipFree(q) == hipSuccess);
 }
 
+// Decomposition policy over a sweep of layer shapes and row counts (the
+// reference checks its own policies the same way, reference
+// tests/test_gemv_policy.cpp:92-97).  The shapes must cover their layer, stay
+// within the kernels' limits, and follow the documented choice rules.
+static void policy_rules() {
+    const uint32_t outputs[] = {128, 256, 384, 1024, 1536, 4096, 5120, 8448, 12288};
+    for (uint32_t I = 128; I <= 16384; I += 128)
+        for (uint32_t N : outputs) {
+            // GEMV: whole 8-block units per split, at most 128 blocks; the
+            // longest split reaching 512 workgroups, else 16 or 8 blocks.
+            const stx::GemvShape sh = stx::gemv_shape(I, N, 4);
+            const uint32_t nb = I / 16, nc = N / 128, units = nb / 8;
+            CHECK(sh.bps % 8 == 0 && sh.bps >= 8 && sh.bps <= 128);
+            CHECK(uint64_t(sh.bps) * sh.splits == nb);
+            const bool reaches = uint64_t(nc) * sh.splits >= 512;
+            for (uint32_t m = 1; m <= 16; ++m) {
+                if (units % m) continue;
+                const bool r = uint64_t(nc) * (nb / (8 * m)) >= 512;
+                if (reaches) CHECK(8 * m <= sh.bps || !r);   // no longer split also reaches it
+                else CHECK(!r);                              // nothing reaches it
+            }
+            if (!reaches) CHECK(sh.bps == 8 || sh.bps == 16);
+            stx::DeviceWeights w;
+            w.input = I;
+            w.output = N;
+            w.bits = 4;
+            for (uint32_t rows = 1; rows <= 8; ++rows) {
+                const uint64_t ws = stx::gemv_workspace_bytes(w, rows);
+                CHECK(ws % 256 == 0 && ws >= stx::gemv_plane_words(w, rows) * 4);
+                CHECK(stx::linear_workspace_bytes(w, rows) >= ws);
+            }
+            // GEMM: the narrow split halves whole 128-channel stages; a wide
+            // split keeps at least eight 64-channel stages per part and never
+            // coexists with the split-tile handoff.
+            const uint32_t ns = stx::narrow_splits(w);
+            CHECK(ns >= 1 && ns <= 16 && (ns & (ns - 1)) == 0 && (I / 128) % ns == 0);
+            const uint64_t pass = stx::gemm_pass_rows(w);
+            CHECK(pass >= 256 && pass % 256 == 0 && pass * I * 2 <= (uint64_t(1) << 30) + 256 * uint64_t(I) * 2);
+            for (uint64_t m : {1ull, 100ull, 255ull, 256ull, 300ull, 512ull, 777ull, 1024ull, 2048ull, 4096ull}) {
+                const uint64_t ws = stx::gemm_workspace_bytes(w, m);
+                CHECK(ws % 256 == 0 && ws >= stx::afrag_bytes(w, m < pass ? m : pass));
+                CHECK(stx::linear_workspace_bytes(w, m) >= ws);
+                if (!stx::gemm_wide(m, w)) {
+                    CHECK(stx::gemm_split_count(w, m) == ns);
+                    continue;
+                }
+                const uint32_t s = stx::wide_splits(m, w);
+                CHECK(s >= 1 && stx::gemm_split_count(w, m) == s);
+                if (s > 1) CHECK((I / 64) / s >= stx::kWideSplitMinStages);
+                const stx::WideSplit sp = stx::wide_split(m, w);
+                CHECK(uint64_t(sp.full) * 256 + uint64_t(sp.half) * 256 == N);
+                const stx::Handoff h = stx::gemm_handoff(m, w);
+                if (h.x) {
+                    const uint64_t tiles = ((m + 255) / 256) * (N / 256);
+                    CHECK(h.x <= 128 && tiles == 256 * uint64_t(h.q) + h.x && tiles % 8 == 0 && s == 1);
+                    CHECK(ws >= stx::afrag_bytes(w, m) + stx::handoff_bytes(h.x) + 4 * h.x);
+                }
+                if (s > 1) CHECK(ws >= stx::afrag_bytes(w, m) + uint64_t(s) * m * N * 4);
+            }
+        }
+    // MoE: whole 8-block units per split, within the kernels' LDS maxima.
+    for (uint32_t input = 128; input <= 16384; input += 128)
+        for (uint32_t max_bps : {uint32_t(stx::MOE_GU_MAX_BPS), uint32_t(stx::MOE_D_MAX_BPS)}) {
+            const stx::MoeSplit ms = stx::moe_split(input, max_bps);
+            CHECK(ms.bps % 8 == 0 && ms.bps >= 8 && ms.bps <= max_bps && uint64_t(ms.bps) * ms.splits * 16 == input);
+        }
+}
+
 int main() {
+    policy_rules();
     context_rules();
     strix_context_desc cd = header<strix_context_desc>();
     strix_context c = nullptr;
