@@ -18,9 +18,18 @@ Also reported on the same JSON line:
   cpu_baseline   the NumPy oracle on the host cores, bounded sample
 
 Timing: each rotation pass (one launch per weight copy) is captured once into
-a HIP graph and replayed; HIP events on the kernels' own stream bracket every
-pass, the reported time per step is the median over passes.  Outputs are
-checked bit-for-bit against an untimed call before and after the timed region.
+a HIP graph and replayed; exactly --steps launches are timed (whole passes plus
+one partial pass), HIP events on the kernels' own stream bracket the region,
+and the time per step is the timed region over the steps.  Replayed outputs
+are checked bit-for-bit against an untimed eager call before and after the
+timed region (`replay_matches_eager`); the headline's output is also checked
+against the NumPy oracle (reference GPU gate) before and after.
+
+call_floor: the same rotation and timing of a plain streaming-read kernel that
+reads the configuration's packed bytes once with the GEMV's grid (the cost of
+one launch that moves those bytes and does nothing else); each GEMV / grouped
+/ MoE cell reports its time as a percentage of that floor beside its
+percentage of HBM peak.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
     python bench.py --pmc-workload     # headline plan + a plain copy, for rocprofv3 --pmc
@@ -103,33 +112,132 @@ class Rotation:
         torch.cuda.synchronize()
         return bool(torch.equal(self.y.view(torch.int32), self.expected.view(torch.int32)))
 
+    def partial(self, n):
+        """A HIP graph of the first n submissions of a pass (captured once per n)."""
+        return capture_partial(self, n)
+
     def close(self):
         del self.graph
+        self.__dict__.pop("_partials", None)
         for p in self.plans:
             p.destroy()
         for w in self.weights:
             w.destroy()
 
 
-def time_rotation(rot, steps, warmup):
-    """Median over passes of (pass time / copies) in ms, HIP events on the plans' stream."""
+def capture_partial(rot, n):
     import torch
-    passes = max(3, -(-steps // rot.copies))
+    cache = rot.__dict__.setdefault("_partials", {})
+    if n not in cache:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=rot.stream):
+            for p in rot.plans[:n]:
+                p.submit()
+        torch.cuda.synchronize()
+        cache[n] = g
+    return cache[n]
+
+
+def time_rotation(rot, steps, warmup):
+    """Time exactly `steps` launches (whole rotation passes, then a partial
+    pass) after >= `warmup` untimed ones; HIP events on the plans' stream.
+    ms = timed region / steps; median_pass_ms = median over whole passes."""
+    import torch
+    full, rem = divmod(steps, rot.copies)
+    part = rot.partial(rem) if rem else None
     for _ in range(max(1, -(-warmup // rot.copies))):
         rot.graph.replay()
     torch.cuda.synchronize()
     ok_before = rot.check()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(passes + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(full + 2)]
     with torch.cuda.stream(rot.stream):
         ev[0].record(rot.stream)
-        for i in range(passes):
+        for i in range(full):
             rot.graph.replay()
             ev[i + 1].record(rot.stream)
+        if part is not None:
+            part.replay()
+        ev[full + 1].record(rot.stream)
     torch.cuda.synchronize()
-    per_pass = [ev[i].elapsed_time(ev[i + 1]) / rot.copies for i in range(passes)]
+    total = ev[0].elapsed_time(ev[full + 1])
+    per_pass = [ev[i].elapsed_time(ev[i + 1]) / rot.copies for i in range(full)]
     ok_after = rot.check()
-    return {"ms": statistics.median(per_pass), "mean_ms": sum(per_pass) / passes,
-            "timed_steps": passes * rot.copies, "passes": passes, "output_check": ok_before and ok_after}
+    return {"ms": total / steps, "median_pass_ms": statistics.median(per_pass) if per_pass else None,
+            "timed_steps": steps, "passes": full + (rem > 0), "output_check": ok_before and ok_after}
+
+
+class FloorRotation:
+    """Call floor: distinct device buffers of `nbytes` each (>= 1 GiB in all), a
+    pass = one streaming-read launch per buffer (`workgroups` x 256 threads),
+    or per launch list entry (bytes, workgroups) when several launches make
+    one step; captured in a HIP graph like the plan rotations."""
+
+    def __init__(self, ctx, launches, min_bytes=ROTATION_BYTES):
+        import torch
+        from strix_trellis import runtime
+        step_bytes = sum(b for b, _ in launches)
+        self.copies = max(2, -(-min_bytes // step_bytes))
+        self.stream = torch.cuda.Stream()
+        self.bufs = [[torch.full((b,), 0x5A, dtype=torch.uint8, device="cuda:0") for b, _ in launches]
+                     for _ in range(self.copies)]
+        self.sink = torch.zeros(max(w for _, w in launches), dtype=torch.int32, device="cuda:0")
+        ctx_ = ctx
+
+        class _Submit:
+            def __init__(self, bufs):
+                self.bufs = bufs
+
+            def submit(self):
+                for buf, (b, wg) in zip(self.bufs, launches):
+                    runtime.stream_read(ctx_, buf, b, wg, self.sink, stream=stream)
+        stream = self.stream
+        _Submit.sink = self.sink
+        self.plans = [_Submit(b) for b in self.bufs]
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            for p in self.plans:
+                p.submit()
+        torch.cuda.synchronize()
+
+    def check(self):
+        return True
+
+    partial = Rotation.partial
+
+    def close(self):
+        del self.graph
+        self.__dict__.pop("_partials", None)
+        self.bufs = None
+
+
+def call_floor(ctx, launches, steps, warmup):
+    """Median-free floor per step in us for `launches` = [(bytes, workgroups)]."""
+    rot = FloorRotation(ctx, launches)
+    try:
+        t = time_rotation(rot, steps, warmup)
+    finally:
+        rot.close()
+    return round(t["ms"] * 1e3, 3)
+
+
+def gemv_grid(ctx, I, N, groups=1):
+    """Workgroups of the single-launch GEMV for a layer: column groups x splits."""
+    return groups * (N // 128) * gemv_splits(ctx, I, N)
+
+
+_SPLITS = {}
+
+
+def gemv_splits(ctx, I, N):
+    """Split count of the GEMV core for I x N, asked of the library (cached)."""
+    if (I, N) not in _SPLITS:
+        import synth
+        from strix_trellis import runtime
+        tr, suh, svh, _ = synth.layer(I, N, 1, 1)
+        w = runtime.Weights(ctx, tr, suh, svh, None, "mul1")
+        _SPLITS[(I, N)] = w.gemv_shape()[1]
+        w.destroy()
+    return _SPLITS[(I, N)]
 
 
 _LIBRARY = {}
@@ -177,18 +285,43 @@ def library_fp16(M, I, N, passes=5):
     return out
 
 
-def bench_gemv(ctx, I, N, K, R, steps, warmup, seed):
+def oracle_gate(got, ref):
+    """The reference GPU gate (maxabs <= 5e-4 * max(1, max|ref|), nrmse <= 3e-5)."""
+    import synth
+    maxabs, nrmse = synth.gate_values(got, ref)
+    bound = 5e-4 * max(1.0, float(abs(ref).max()))
+    return {"maxabs": float(f"{maxabs:.3e}"), "nrmse": float(f"{nrmse:.3e}"),
+            "pass": bool(maxabs <= bound and nrmse <= 3e-5)}
+
+
+def bench_gemv(ctx, I, N, K, R, steps, warmup, seed, oracle=False):
     rot = Rotation(ctx, I, N, K, R, seed, "gemv")
+    gate = {}
     try:
+        if oracle:
+            from oracle import linear
+            import synth
+            tr, suh, svh, _ = synth.layer(I, N, K, seed)
+            ref = linear.matmul_fp32(rot.x.cpu().numpy(), tr, suh, svh, K, "mul1")
+            gate["before"] = oracle_gate(rot.expected.cpu().numpy(), ref)
         t = time_rotation(rot, steps, warmup)
+        if oracle:
+            gate["after"] = oracle_gate(rot.y.cpu().numpy(), ref)
     finally:
         rot.close()
     gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
     lib = library_fp16(R, I, N)
-    return {"I": I, "N": N, "K": K, "R": R, "us": round(t["ms"] * 1e3, 3), "packed_GBps": round(gbps, 1),
-            "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "launches": rot.launches,
-            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"],
-            "fp16_library_us": lib["us"], "speedup_vs_fp16_library": round(lib["us"] / (t["ms"] * 1e3), 2)}
+    floor = call_floor(ctx, [(rot.packed, gemv_grid(ctx, I, N))], steps, warmup)
+    out = {"I": I, "N": N, "K": K, "R": R, "us": round(t["ms"] * 1e3, 3), "packed_GBps": round(gbps, 1),
+           "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "call_floor_us": floor,
+           "pct_call_floor": round(100 * floor / (t["ms"] * 1e3), 1), "launches": rot.launches,
+           "rotation_copies": rot.copies, "timed_steps": t["timed_steps"],
+           "median_pass_us": round(t["median_pass_ms"] * 1e3, 3) if t["median_pass_ms"] else None,
+           "replay_matches_eager": t["output_check"],
+           "fp16_library_us": lib["us"], "speedup_vs_fp16_library": round(lib["us"] / (t["ms"] * 1e3), 2)}
+    if oracle:
+        out["oracle_gate"] = gate
+    return out
 
 
 def bench_gemm(ctx, M, I, N, K, steps, warmup, seed):
@@ -202,7 +335,7 @@ def bench_gemm(ctx, M, I, N, K, steps, warmup, seed):
     lib_tflops = 2.0 * M * I * N / (lib["us"] * 1e-6) / 1e12
     return {"M": M, "I": I, "N": N, "K": K, "us": round(t["ms"] * 1e3, 2), "TFLOPs": round(tflops, 1),
             "pct_fp16_peak": round(100 * tflops / FP16_PEAK_TFLOPS, 1), "launches": rot.launches,
-            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"],
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "replay_matches_eager": t["output_check"],
             "fp16_library_us": lib["us"], "fp16_library_pct_peak": round(100 * lib_tflops / FP16_PEAK_TFLOPS, 1),
             "speedup_vs_fp16_library": round(lib["us"] / (t["ms"] * 1e3), 2)}
 
@@ -214,9 +347,11 @@ def bench_grouped(ctx, G, I, N, K, R, steps, warmup, seed):
     finally:
         rot.close()
     gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
+    floor = call_floor(ctx, [(rot.packed, gemv_grid(ctx, I, N, G))], steps, warmup)
     return {"groups": G, "I": I, "N": N, "K": K, "R": R, "us": round(t["ms"] * 1e3, 3),
             "packed_GBps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1),
-            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
+            "call_floor_us": floor, "pct_call_floor": round(100 * floor / (t["ms"] * 1e3), 1),
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "replay_matches_eager": t["output_check"]}
 
 
 class MoeRotation:
@@ -256,9 +391,11 @@ class MoeRotation:
         torch.cuda.synchronize()
 
     check = Rotation.check
+    partial = Rotation.partial
 
     def close(self):
         del self.graph
+        self.__dict__.pop("_partials", None)
         for p in self.plans:
             p.destroy()
         for w in self.weights:
@@ -274,10 +411,16 @@ def bench_moe(ctx, steps, warmup, seed):
     finally:
         rot.close()
     gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
+    per = (2 * I * H + H * I) * K // 8
+    gu, dn = rot.distinct * per * 2 // 3, rot.distinct * per // 3
+    floor = call_floor(ctx, [(gu, 1024), (dn, 1024)], steps, warmup)
     return {"experts": E, "I": I, "H": H, "K": K, "rows": R, "top_k": k, "distinct_experts": rot.distinct,
             "packed_bytes": rot.packed, "us": round(t["ms"] * 1e3, 2), "packed_GBps": round(gbps, 1),
-            "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "launches": 2, "rotation_copies": rot.copies,
-            "timed_steps": t["timed_steps"], "bit_identical": t["output_check"]}
+            "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "call_floor_us": floor,
+            "call_floor_launches": "gate/up bytes then down bytes, 1024 workgroups each",
+            "pct_call_floor": round(100 * floor / (t["ms"] * 1e3), 1), "launches": 2,
+            "rotation_copies": rot.copies, "timed_steps": t["timed_steps"],
+            "replay_matches_eager": t["output_check"]}
 
 
 def cpu_baseline(sample_seconds=12.0):
@@ -375,14 +518,14 @@ def pmc_workload(ctx, launches, which="gemv"):
     ok = rot.check()
     rot.close()
     if which != "gemv":
-        log(f"pmc workload {which}: {launches} launches (bit_identical={ok})")
+        log(f"pmc workload {which}: {launches} launches (replay_matches_eager={ok})")
         return
     src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"pmc workload: {launches} headline launches (bit_identical={ok}), 4 copies of {src.numel() * 4} bytes")
+    log(f"pmc workload: {launches} headline launches (replay_matches_eager={ok}), 4 copies of {src.numel() * 4} bytes")
 
 
 def run_section(ctx, which, steps, warmup):
@@ -437,7 +580,7 @@ def main():
         return
 
     log("headline: GEMV R1 K4 4096x4096")
-    head = bench_gemv(ctx, 4096, 4096, 4, 1, args.steps, args.warmup, synth.BASE_SEED)
+    head = bench_gemv(ctx, 4096, 4096, 4, 1, args.steps, args.warmup, synth.BASE_SEED, oracle=True)
     log(json.dumps(head))
     small_steps, small_warm = max(256, args.steps // 8), max(32, args.warmup // 8)
     sweep, gemm, grouped, moe_cell = [], [], [], None
@@ -481,7 +624,9 @@ def main():
         "config": {"workload": "decode GEMV R1, EXL3 K4 mul1, I=N=4096, prepared single-launch plan, "
                                f"cold rotation over {head['rotation_copies']} weight copies (>=1 GiB)",
                    "us_per_call": head["us"], "pct_hbm_peak": head["pct_hbm_peak"],
-                   "bit_identical": head["bit_identical"], "fp16_library_us": head["fp16_library_us"],
+                   "replay_matches_eager": head["replay_matches_eager"], "oracle_gate": head.get("oracle_gate"),
+                   "call_floor_us": head["call_floor_us"], "pct_call_floor": head["pct_call_floor"],
+                   "fp16_library_us": head["fp16_library_us"],
                    "speedup_vs_fp16_library": head["speedup_vs_fp16_library"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _traffic(),

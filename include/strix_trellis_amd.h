@@ -64,6 +64,33 @@ strix_status strix_amd_swiglu(strix_context context, const float *gate, const fl
  * 0 restores the default.  Outputs are bit-identical either way. */
 strix_status strix_amd_set_gemm_handoff(strix_context context, uint32_t always_take_over);
 
+/* Single-launch GEMV plans (linear plans with rows 1-8, grouped plans, TP
+ * dense plans): the workgroup of each output group's last input split waits,
+ * with a bounded poll, for the other splits' published partial sums.  A wait
+ * that runs out writes NaN outputs and sets STRIX_AMD_GEMV_GAVE_UP in the
+ * plan's sticky status word; later submissions of the plan stay correct
+ * (partials carry a per-launch tag, so a late one is never folded).
+ * poll_limit = rounds of that wait for every later submission on the context
+ * (a round is a few hundred ns); 0 makes every finisher give up at once (test
+ * hook).  strix_amd_set_gemv_poll_limit(context, STRIX_AMD_GEMV_POLL_DEFAULT)
+ * restores the default. */
+#define STRIX_AMD_GEMV_POLL_DEFAULT 4194304u
+#define STRIX_AMD_GEMV_GAVE_UP 1u
+strix_status strix_amd_set_gemv_poll_limit(strix_context context, uint32_t poll_limit);
+
+/* Sticky status flags of a single-launch plan (0 for plans that need no
+ * wait), read after synchronising the plan's stream; clear != 0 also resets
+ * them (enqueued before the synchronisation). */
+strix_status strix_amd_plan_status(strix_linear_plan plan, uint32_t clear, uint32_t *flags);
+strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan plan, uint32_t clear, uint32_t *flags);
+
+/* Measured call floor: one kernel of `workgroups` x 256 threads reads `bytes`
+ * device bytes from src once (16-byte loads, the decode GEMV's load depth) and
+ * stores one word per workgroup into sink.  bytes must be a multiple of
+ * 16 * workgroups; nothing else is read or written. */
+strix_status strix_amd_stream_read(strix_context context, const void *src, uint64_t bytes, uint32_t workgroups,
+    uint32_t *sink, const strix_stream *stream);
+
 #ifdef __cplusplus
 }
 #endif

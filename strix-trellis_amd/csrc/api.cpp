@@ -543,38 +543,80 @@ strix_status strix_linear_plan_create(strix_context c, const strix_matmul_desc* 
     plan->gemm = gemm;
     plan->call = make_call(*d, call.rows, d->workspace);
     plan->launches = 0;
-    const uint64_t words = (!gemm && call.rows) ? stx::gemv_plane_words(w->dev, call.rows) : 0;
-    if (words) {
-        void* p = nullptr;
-        hipError_t e = hipMalloc(&p, words * sizeof(uint32_t));
-        if (e == hipSuccess) e = stx::launch_fill_u32(static_cast<uint32_t*>(p), stx::GEMV_PLANE_EMPTY, words, hs);
-        if (e == hipSuccess) e = hipStreamSynchronize(hs);
-        if (e == hipSuccess) {
-            try {
-                w->counter_arrays.push_back(p);   // freed with the weights
-            } catch (...) {
-                e = hipErrorOutOfMemory;
-            }
-        }
-        if (e != hipSuccess) {
-            if (p) (void)hipFree(p);
+    if (!gemm && call.rows) {
+        s = make_fused_state(w, call.rows, hs, plan->fused);
+        if (s != STRIX_SUCCESS) {
             delete plan;
-            return from_hip(e);
+            return s;
         }
-        plan->planes = static_cast<float*>(p);
     }
-    if (call.rows) plan->launches = stx::linear_launch_count(w->dev, call.rows, gemm, plan->planes != nullptr);
+    if (call.rows) plan->launches = stx::linear_launch_count(w->dev, call.rows, gemm, plan->fused.planes != nullptr);
     ++w->plans;
     *out = plan;
     return STRIX_SUCCESS;
 }
+
+}  // extern "C"
+
+namespace stx_api {
+
+hipError_t init_fused_state(void* base, uint64_t bytes, uint64_t planes_offset, hipStream_t hs) {
+    uint32_t* words = static_cast<uint32_t*>(base);
+    hipError_t e = stx::launch_fill_u32(words, 0u, planes_offset / 4, hs);
+    if (e == hipSuccess)
+        e = stx::launch_fill_u32(words + planes_offset / 4, stx::GEMV_PLANE_EMPTY, (bytes - planes_offset) / 4, hs);
+    return e;
+}
+
+strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, stx::FusedState& out) {
+    out = {};
+    const uint64_t bytes = stx::fused_state_bytes(w->dev, rows, 1);
+    if (!bytes) return STRIX_SUCCESS;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipSuccess) e = init_fused_state(p, bytes, stx::fused_planes_offset(w->dev, 1), hs);
+    if (e == hipSuccess) e = hipStreamSynchronize(hs);
+    if (e == hipSuccess) {
+        try {
+            w->counter_arrays.push_back(p);   // freed with the weights
+        } catch (...) {
+            e = hipErrorOutOfMemory;
+        }
+    }
+    if (e != hipSuccess) {
+        if (p) (void)hipFree(p);
+        return from_hip(e);
+    }
+    out = stx::fused_state_at(p, w->dev, rows, 1);
+    return STRIX_SUCCESS;
+}
+
+strix_status read_fused_status(const stx::FusedState& st, hipStream_t hs, uint32_t* flags, uint32_t clear) {
+    *flags = 0;
+    if (!st.status) return STRIX_SUCCESS;
+    uint32_t v = 0;
+    hipError_t e = hipMemcpyAsync(&v, st.status, sizeof(v), hipMemcpyDeviceToHost, hs);
+    if (e == hipSuccess && clear) e = stx::launch_fill_u32(st.status, 0u, 1, hs);
+    if (e == hipSuccess) e = hipStreamSynchronize(hs);
+    if (e != hipSuccess) return from_hip(e);
+    *flags = v;
+    return STRIX_SUCCESS;
+}
+
+}  // namespace stx_api
+
+extern "C" {
 
 strix_status strix_linear_plan_submit(strix_linear_plan p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
     const strix_status s = context_ok(p->owner);
     if (s != STRIX_SUCCESS || !p->call.rows) return s;
     const stx::DeviceWeights& w = p->weights->dev;
-    if (!p->gemm && p->planes) return from_hip(stx::launch_gemv_fused(w, p->call, p->planes, p->stream));
+    if (!p->gemm && p->fused.planes) {
+        stx::LinearCall call = p->call;
+        call.gemv_poll_limit = p->owner->gemv_poll_limit;
+        return from_hip(stx::launch_gemv_fused(w, call, p->fused, p->stream));
+    }
     return from_hip(stx::launch_linear(w, p->call, p->gemm, p->stream));
 }
 
@@ -698,6 +740,34 @@ strix_status strix_amd_plan_launches(strix_linear_plan p, uint32_t* launches) {
     if (!p || !launches) return STRIX_ERROR_INVALID_ARGUMENT;
     *launches = p->launches;
     return STRIX_SUCCESS;
+}
+
+strix_status strix_amd_set_gemv_poll_limit(strix_context c, uint32_t poll_limit) {
+    const strix_status s = context_ok(c);
+    if (s != STRIX_SUCCESS) return s;
+    c->gemv_poll_limit = poll_limit;
+    return STRIX_SUCCESS;
+}
+
+strix_status strix_amd_plan_status(strix_linear_plan p, uint32_t clear, uint32_t* flags) {
+    if (flags) *flags = 0;
+    if (!p || !flags) return STRIX_ERROR_INVALID_ARGUMENT;
+    const strix_status s = context_ok(p->owner);
+    if (s != STRIX_SUCCESS) return s;
+    return read_fused_status(p->fused, p->stream, flags, clear);
+}
+
+strix_status strix_amd_stream_read(strix_context c, const void* src, uint64_t bytes, uint32_t workgroups,
+                                   uint32_t* sink, const strix_stream* stream) {
+    strix_status s = context_ok(c);
+    if (s != STRIX_SUCCESS) return s;
+    hipStream_t hs{};
+    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
+    if (!workgroups || !bytes || bytes % (16ull * workgroups) || bytes / workgroups >= (uint64_t(1) << 31))
+        return STRIX_ERROR_INVALID_ARGUMENT;
+    if ((s = device_range_ok(c, src, bytes, 16)) != STRIX_SUCCESS) return s;
+    if ((s = device_range_ok(c, sink, uint64_t(workgroups) * 4, 4)) != STRIX_SUCCESS) return s;
+    return from_hip(stx::launch_stream_read(src, bytes, workgroups, sink, hs));
 }
 
 strix_status strix_amd_set_gemm_handoff(strix_context c, uint32_t always_take_over) {

@@ -3,14 +3,15 @@
 //
 //   output[r][g*ogs + n] = Linear_g(input[r][g*igs + i]),  alpha 1, beta 0, rows 1..8
 //
-// Every group runs the generic GEMV core of its geometry in one launch (grid z =
-// group), so each row has exactly the bits of that row submitted alone through
+// Every group runs the generic GEMV core of its geometry in one launch (the
+// grid covers every group's column groups), so each row has exactly the bits
+// of that row submitted alone through
 // strix_gemv (STRIX_GEMV_ROW_INVARIANT_R1).  Workspace layout, all offsets a
 // function of the geometry only:
-//   [group table: kMaxGroups entries][partials: G * S * rows * N f32]
-// The workspace is dedicated to the plan: creation uploads the table, fills
-// the partial planes with GEMV_PLANE_EMPTY and synchronises the stream; each
-// completed submission leaves the planes EMPTY again (one launch per submit).
+//   [group table: kMaxGroups entries][single-launch state of G groups]
+// (the state's status word, launch epochs and tagged planes: backend.hpp).
+// The workspace is dedicated to the plan: creation uploads the table,
+// initialises the state and synchronises the stream; one launch per submission.
 #include "api_internal.hpp"
 
 #include <new>
@@ -23,7 +24,7 @@ constexpr uint64_t kAlign = STRIX_TRELLIS_WORKSPACE_ALIGNMENT;
 uint64_t align_up(uint64_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
 struct GroupLayout {
-    uint64_t table_offset = 0, partial_offset = 0, plane_words = 0, bytes = 0;
+    uint64_t table_offset = 0, state_offset = 0, state_bytes = 0, bytes = 0;
 };
 
 struct Validated {
@@ -80,12 +81,11 @@ strix_status validate(strix_context c, const strix_grouped_gemv_desc* d, Validat
     for (strix_weights w : v.weights)
         if (overlaps(d->input, v.input_bytes, w->base, w->bytes) || overlaps(d->output, v.output_bytes, w->base, w->bytes))
             return STRIX_ERROR_INVALID_ARGUMENT;
-    const stx::GemvShape sh = stx::gemv_shape(uint32_t(I), uint32_t(N), v.geometry.bits);
     GroupLayout& L = v.layout;
     L.table_offset = 0;
-    L.partial_offset = align_up(kMaxGroups * sizeof(stx::GroupWeights));
-    L.plane_words = sh.splits > 1 ? uint64_t(sh.splits) * rows * N * G : 0;
-    L.bytes = L.partial_offset + align_up(L.plane_words * 4);
+    L.state_offset = align_up(kMaxGroups * sizeof(stx::GroupWeights));
+    L.state_bytes = stx::fused_state_bytes(v.geometry, rows, uint32_t(G));
+    L.bytes = L.state_offset + align_up(L.state_bytes);
     return STRIX_SUCCESS;
 }
 }  // namespace
@@ -96,6 +96,7 @@ struct strix_grouped_gemv_plan_impl {
     stx::DeviceWeights geometry{};
     stx::LinearCall call{};
     const stx::GroupWeights* table = nullptr;
+    stx::FusedState fused{};   // null when one split suffices
     uint64_t xgs = 0, ygs = 0;
     hipStream_t stream{};
 };
@@ -152,9 +153,9 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
     p->table = reinterpret_cast<const stx::GroupWeights*>(base + v.layout.table_offset);
     hipError_t e = hipMemcpyAsync(base + v.layout.table_offset, table.data(), table.size() * sizeof(table[0]),
                                   hipMemcpyHostToDevice, hs);
-    if (e == hipSuccess)
-        e = stx::launch_fill_u32(reinterpret_cast<uint32_t*>(base + v.layout.partial_offset), stx::GEMV_PLANE_EMPTY,
-                                 v.layout.plane_words, hs);
+    if (e == hipSuccess && v.layout.state_bytes)
+        e = init_fused_state(base + v.layout.state_offset, v.layout.state_bytes,
+                             stx::fused_planes_offset(v.geometry, uint32_t(v.weights.size())), hs);
     const hipError_t done = hipStreamSynchronize(hs);
     if (e != hipSuccess || done != hipSuccess) {
         delete p;
@@ -172,7 +173,9 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
     p->call.y_row_stride = v.yrs;
     p->call.alpha = 1.0f;
     p->call.beta = 0.0f;
-    p->call.workspace = base + v.layout.partial_offset;
+    p->call.workspace = nullptr;
+    if (v.layout.state_bytes)
+        p->fused = stx::fused_state_at(base + v.layout.state_offset, v.geometry, v.rows, uint32_t(v.weights.size()));
     for (strix_weights w : v.weights) ++w->plans;
     *out = p;
     return STRIX_SUCCESS;
@@ -182,8 +185,21 @@ strix_status strix_grouped_gemv_plan_submit(strix_grouped_gemv_plan p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
     const strix_status s = context_ok(p->owner);
     if (s != STRIX_SUCCESS) return s;
-    return from_hip(stx::launch_gemv_grouped(p->geometry, p->table, uint32_t(p->retained.size()), p->call, p->xgs,
-                                             p->ygs, true, p->stream));
+    stx::LinearCall call = p->call;
+    call.gemv_poll_limit = p->owner->gemv_poll_limit;
+    const stx::FusedState* st = p->fused.planes ? &p->fused : nullptr;
+    if (!st && stx::gemv_shape(p->geometry.input, p->geometry.output, p->geometry.bits).splits > 1)
+        return STRIX_ERROR_BACKEND;
+    return from_hip(stx::launch_gemv_grouped(p->geometry, p->table, uint32_t(p->retained.size()), call, p->xgs,
+                                             p->ygs, st, p->stream));
+}
+
+strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan p, uint32_t clear, uint32_t* flags) {
+    if (flags) *flags = 0;
+    if (!p || !flags) return STRIX_ERROR_INVALID_ARGUMENT;
+    const strix_status s = context_ok(p->owner);
+    if (s != STRIX_SUCCESS) return s;
+    return read_fused_status(p->fused, p->stream, flags, clear);
 }
 
 strix_status strix_grouped_gemv_plan_destroy(strix_grouped_gemv_plan p) {

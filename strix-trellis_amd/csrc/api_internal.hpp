@@ -12,6 +12,7 @@ struct strix_context_impl {
     int compute_units = 0;
     uint64_t weights_live = 0;
     uint32_t gemm_handoff_poll = 4096;   // LinearCall::handoff_poll_limit of calls made on it
+    uint32_t gemv_poll_limit = stx::GEMV_DEFAULT_POLL_LIMIT;   // single-launch GEMV finishers
 };
 
 struct strix_weights_impl {
@@ -20,9 +21,9 @@ struct strix_weights_impl {
     void* base = nullptr;     // single private allocation: trellis | suh | svh | bias
     uint64_t bytes = 0;
     uint64_t plans = 0;       // live plans retaining these weights
-    // Single-launch state (partial planes) of plans created on these weights.  Graphs
-    // captured from a plan may replay after the plan is destroyed, so the
-    // arrays live until the weights are destroyed.
+    // Single-launch state (tagged planes, epochs, status) of plans created on
+    // these weights.  Graphs captured from a plan may replay after the plan is
+    // destroyed, so the arrays live until the weights are destroyed.
     std::vector<void*> counter_arrays;
 };
 
@@ -32,7 +33,7 @@ struct strix_linear_plan_impl {
     stx::LinearCall call{};
     hipStream_t stream{};
     bool gemm = false;
-    float* planes = nullptr;    // dedicated split planes of the single-launch GEMV
+    stx::FusedState fused{};    // single-launch GEMV state (null when one split suffices)
     uint32_t launches = 0;
 };
 
@@ -73,5 +74,14 @@ strix_status call_ok(strix_context c, const strix_matmul_desc* d, Call& call);
 strix_status storage_ok(strix_context c, const strix_matmul_desc& d, const Call& call, const void* workspace,
                         uint64_t bytes);
 stx::LinearCall make_call(const strix_matmul_desc& d, uint64_t rows, void* workspace);
+// Enqueue the initial contents of a single-launch state of `bytes` at base:
+// status and epochs 0, every plane word GEMV_PLANE_EMPTY.
+hipError_t init_fused_state(void* base, uint64_t bytes, uint64_t planes_offset, hipStream_t hs);
+// Initialised single-launch GEMV state for `rows` rows on `w` (none when one
+// split suffices), owned by the weights; the stream is synchronised.
+strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, stx::FusedState& out);
+// Sticky status word of a single-launch state: read (synchronising `hs`) and
+// optionally cleared.
+strix_status read_fused_status(const stx::FusedState& st, hipStream_t hs, uint32_t* flags, uint32_t clear);
 
 }  // namespace stx_api

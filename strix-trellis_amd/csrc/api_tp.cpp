@@ -31,7 +31,7 @@ namespace {
 struct TpMember {
     strix_weights weights = nullptr;
     stx::LinearCall call{};
-    float* planes = nullptr;
+    stx::FusedState fused{};
 };
 }  // namespace
 
@@ -110,28 +110,13 @@ strix_status member_ok(strix_context c, strix_weights w, const strix_tensor_desc
     return STRIX_SUCCESS;
 }
 
-// Plane memory for every member (freed with its weights), EMPTY-filled.
+// Single-launch state for every member (freed with its weights), zeroed.
 strix_status arm(std::vector<TpMember>& members, hipStream_t hs) {
     for (TpMember& m : members) {
-        const uint64_t words = stx::gemv_plane_words(m.weights->dev, m.call.rows);
-        if (!words) continue;
-        void* p = nullptr;
-        hipError_t e = hipMalloc(&p, words * 4);
-        if (e == hipSuccess) e = stx::launch_fill_u32(static_cast<uint32_t*>(p), stx::GEMV_PLANE_EMPTY, words, hs);
-        if (e == hipSuccess) {
-            try {
-                m.weights->counter_arrays.push_back(p);
-            } catch (...) {
-                e = hipErrorOutOfMemory;
-            }
-        }
-        if (e != hipSuccess) {
-            if (p) (void)hipFree(p);
-            return e == hipErrorOutOfMemory ? STRIX_ERROR_OUT_OF_MEMORY : from_hip(e);
-        }
-        m.planes = static_cast<float*>(p);
+        const strix_status s = make_fused_state(m.weights, m.call.rows, hs, m.fused);
+        if (s != STRIX_SUCCESS) return s;
     }
-    return from_hip(hipStreamSynchronize(hs));
+    return STRIX_SUCCESS;
 }
 
 template <class Plan>
@@ -150,7 +135,10 @@ strix_status finish_create(Plan* p, strix_context c, hipStream_t hs) {
 
 hipError_t launch_member(const TpMember& m, hipStream_t hs) {
     const stx::DeviceWeights& w = m.weights->dev;
-    return m.planes ? stx::launch_gemv_fused(w, m.call, m.planes, hs) : stx::launch_gemv(w, m.call, hs);
+    if (!m.fused.planes) return stx::launch_gemv(w, m.call, hs);
+    stx::LinearCall call = m.call;
+    call.gemv_poll_limit = m.weights->owner->gemv_poll_limit;
+    return stx::launch_gemv_fused(w, call, m.fused, hs);
 }
 
 strix_status dense_create(strix_context c, const strix_matmul_desc* d, const strix_stream* stream,

@@ -41,11 +41,33 @@ GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t bits);
 uint64_t gemv_workspace_bytes(const DeviceWeights& w, uint32_t rows);
 uint64_t gemm_workspace_bytes(const DeviceWeights& w, uint64_t rows);
 uint64_t linear_workspace_bytes(const DeviceWeights& w, uint64_t rows);
-// Single-launch GEMV: F32 words of the dedicated partial planes a plan owns
-// ([splits][rows][N], 0 when one split suffices).  Between launches every word
-// holds GEMV_PLANE_EMPTY.
+// Single-launch GEMV state, dedicated to one plan (one allocation, 256-byte
+// aligned pieces):
+//   status  sticky flags (GEMV_STATUS_*), set by a finisher that gave up;
+//   epochs  one launch counter per 128-column group ([groups][N/128] u32);
+//   planes  two sets of partial sums of splits 0..S-2, per column group
+//           ([2][groups * N/128][S-1][rows][128] F32).
+// Created with status and epochs 0 and every plane word GEMV_PLANE_EMPTY.  A
+// launch of column group g with epoch e uses set e & 1: its finisher polls
+// that set until no word is EMPTY, and re-arms (EMPTY-fills) the other set,
+// which the previous launch used and which no workgroup of this launch
+// touches; then it advances epochs[g].  A partial published late (after a
+// finisher gave up) lands in a set the next launch leaves alone and re-arms.
+struct FusedState {
+    uint32_t* status = nullptr;
+    uint32_t* epochs = nullptr;
+    float* planes = nullptr;
+};
 constexpr uint32_t GEMV_PLANE_EMPTY = 0xFFFFFFFFu;
-uint64_t gemv_plane_words(const DeviceWeights& w, uint64_t rows);
+constexpr uint32_t GEMV_STATUS_GAVE_UP = 1u;
+// Poll rounds before a finisher gives up (a few hundred ms); 0 gives up at
+// once without polling (test hook).
+constexpr uint32_t GEMV_DEFAULT_POLL_LIMIT = 1u << 22;
+// Bytes of the state (0 when one split suffices: the launch needs none), and
+// where its pieces start; the planes run from planes_offset to the end.
+uint64_t fused_state_bytes(const DeviceWeights& w, uint64_t rows, uint32_t groups);
+uint64_t fused_planes_offset(const DeviceWeights& w, uint32_t groups);
+FusedState fused_state_at(void* base, const DeviceWeights& w, uint64_t rows, uint32_t groups);
 
 struct LinearCall {
     const float* x = nullptr;
@@ -59,25 +81,27 @@ struct LinearCall {
     // Prefill GEMM split-tile handoff: polls before the second workgroup of a
     // split tile takes it over from K = 0 (UINT32_MAX: always, a test hook).
     uint32_t handoff_poll_limit = 4096;
+    // Single-launch GEMV: poll rounds of a finisher before it gives up.
+    uint32_t gemv_poll_limit = GEMV_DEFAULT_POLL_LIMIT;
 };
 
 // Generic GEMV (rows 1..8): core kernel + finishing kernel, no counters.
 hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
 // Single-launch GEMV: the workgroup of the last split of each 128-output group
-// waits for the other splits' planes and finishes.  `planes` must hold
-// GEMV_PLANE_EMPTY in every word on entry and does again when the launch ends.
-hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, float* planes, hipStream_t stream);
+// waits for the other splits' tagged planes and finishes (state as above).
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, const FusedState& state,
+                             hipStream_t stream);
 // Second launch of a split-K core: folds planes[S][rows][N] (row stride N) in
 // ascending split order from +0, then H32 and the output stage into call.y.
 hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& call, const float* planes, uint32_t splits,
                                hipStream_t stream);
 
 // Grouped GEMV over `groups` weights of one geometry (table in device memory).
-// single_launch: the planes are call.workspace, dedicated and EMPTY-filled as
-// for launch_gemv_fused; otherwise a finishing kernel folds them.
+// With `state` (dedicated to the plan, as for launch_gemv_fused) one launch;
+// without, the F32 planes are call.workspace and a finishing kernel folds them.
 hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
                                const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
-                               bool single_launch, hipStream_t stream);
+                               const FusedState* state, hipStream_t stream);
 // Prefill path (any row count): input stage to FP16 in the workspace, then the
 // MFMA core with the fused output stage.
 hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
@@ -95,5 +119,10 @@ hipError_t launch_input_stage(const DeviceWeights& w, const float* x, uint64_t r
 hipError_t launch_output_stage(const DeviceWeights& w, const float* core, uint64_t rows, float* y,
                                float alpha, float beta, hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStream_t stream);
+// Streaming read of `bytes` (a multiple of 16) by `workgroups` x 256 threads,
+// 16-byte loads, nothing stored but one word per workgroup into sink: the
+// measured call floor of a kernel that reads that many bytes once.
+hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* sink,
+                              hipStream_t stream);
 
 }  // namespace stx

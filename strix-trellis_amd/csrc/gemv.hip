@@ -20,7 +20,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
     const GroupWeights gw = group_weights(a, z);
     float* y = a.y + z * a.y_group_stride;
     const float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
-    finish_columns<true>(a, gw, column_operands(gw, c), y, c, a.splits, [&](int s, int r) -> const float* {
+    finish_columns(a, gw, column_operands(gw, c), y, c, a.splits, [&](int s, int r) -> const float* {
         return plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c;
     });
 }
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void plane_finish_kernel(GemvArgs a) 
 
 static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table, uint32_t groups,
                               const LinearCall& call, uint64_t xg, uint64_t yg, float* planes,
-                              uint32_t mode, hipStream_t stream) {
+                              const FusedState* state, hipStream_t stream) {
     const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
     GemvLaunch l{};
     GemvArgs& a = l.args;
@@ -89,6 +89,7 @@ static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table,
     a.x = call.x;
     a.y = call.y;
     a.partials = planes;
+    if (state) a.state = *state;
     a.x_row_stride = call.x_row_stride;
     a.y_row_stride = call.y_row_stride;
     a.x_group_stride = xg;
@@ -100,9 +101,13 @@ static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table,
     a.bps = sh.bps;
     a.alpha = call.alpha;
     a.beta = call.beta;
-    a.mode = mode;
+    a.mode = state ? 1 : 0;
+    a.poll_limit = call.gemv_poll_limit;
+    a.ncg = w.output / 128;
+    a.groups = groups;
     l.rows_template = rows_template(call.rows);
-    l.grid = dim3(w.output / 128, sh.splits, groups);
+    // Split-major 1-D grid (gemv_slot).
+    l.grid = dim3(a.ncg * groups * sh.splits, 1, 1);
     l.codebook = w.codebook;
     l.lds = size_t(l.rows_template) * (32u * sh.bps + 2048u);
     l.stream = stream;
@@ -110,15 +115,19 @@ static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table,
 }
 
 // The per-split buffer resource spans bps rows of tiles and must stay below
-// 2^31 bytes (its out-of-range sentinel); the split count is a grid dimension.
-static bool gemv_fits(const DeviceWeights& w) {
+// 2^31 bytes (its out-of-range sentinel); the 1-D grid holds every column
+// group x split; the tagged planes of one column group fit a buffer resource.
+static bool gemv_fits(const DeviceWeights& w, uint32_t groups, uint64_t rows) {
     const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
-    return uint64_t(sh.bps) * (w.output / 16) * 32u * w.bits < (uint64_t(1) << 31) && sh.splits <= 65535;
+    const uint64_t cgs = uint64_t(w.output / 128) * groups;
+    return uint64_t(sh.bps) * (w.output / 16) * 32u * w.bits < (uint64_t(1) << 31) &&
+           cgs * sh.splits < (uint64_t(1) << 31) &&
+           uint64_t(sh.splits) * rows * 128 * 8 < (uint64_t(1) << 31);
 }
 
 hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream) {
-    if (!gemv_fits(w)) return hipErrorInvalidValue;
-    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, static_cast<float*>(call.workspace), 0, stream);
+    if (!gemv_fits(w, 1, call.rows)) return hipErrorInvalidValue;
+    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, static_cast<float*>(call.workspace), nullptr, stream);
     hipError_t e = gemv_table[w.bits - 1](l);
     if (e != hipSuccess || l.args.splits == 1) return e;
     hipLaunchKernelGGL(gemv_finish_kernel, dim3(w.output / 128, 1, 1), dim3(GEMV_THREADS), 0, stream, l.args);
@@ -145,20 +154,21 @@ hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& call, c
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, float* planes, hipStream_t stream) {
-    if (!gemv_fits(w)) return hipErrorInvalidValue;
-    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, planes, 1, stream);
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, const FusedState& state,
+                             hipStream_t stream) {
+    if (!gemv_fits(w, 1, call.rows)) return hipErrorInvalidValue;
+    GemvLaunch l = make_launch(w, nullptr, 1, call, 0, 0, nullptr, &state, stream);
     return gemv_table[w.bits - 1](l);
 }
 
 hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
                                const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
-                               bool single_launch, hipStream_t stream) {
-    if (!gemv_fits(geometry)) return hipErrorInvalidValue;
+                               const FusedState* state, hipStream_t stream) {
+    if (!gemv_fits(geometry, groups, call.rows)) return hipErrorInvalidValue;
     GemvLaunch l = make_launch(geometry, table, groups, call, x_group_stride, y_group_stride,
-                               static_cast<float*>(call.workspace), single_launch ? 1 : 0, stream);
+                               static_cast<float*>(call.workspace), state, stream);
     hipError_t e = gemv_table[geometry.bits - 1](l);
-    if (e != hipSuccess || single_launch || l.args.splits == 1) return e;
+    if (e != hipSuccess || state || l.args.splits == 1) return e;
     hipLaunchKernelGGL(gemv_finish_kernel, dim3(geometry.output / 128, 1, groups), dim3(GEMV_THREADS), 0,
                        stream, l.args);
     return hipGetLastError();
@@ -211,6 +221,42 @@ hipError_t launch_output_stage(const DeviceWeights& w, const float* core, uint64
     if (!rows) return hipSuccess;
     hipLaunchKernelGGL(output_stage_kernel, dim3(w.output / 128, rows), dim3(64), 0, stream, core, w.svh, w.bias,
                        w.output, alpha, beta, y);
+    return hipGetLastError();
+}
+
+// Streaming read: workgroup b reads its contiguous 1/workgroups of the bytes
+// with 16-byte buffer loads, up to four per lane in flight (the decode GEMV's
+// prefetch depth), and folds them with XOR; one word per workgroup is stored.
+__global__ __launch_bounds__(256) void stream_read_kernel(const unsigned char* src, uint64_t bytes,
+                                                          uint32_t* sink) {
+    const uint64_t per = bytes / gridDim.x;   // a multiple of 16 (checked by the launcher)
+    const auto rsrc = make_rsrc(src + uint64_t(blockIdx.x) * per, uint32_t(per));
+    const uint32_t n = uint32_t(per / 16);
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (uint32_t i = threadIdx.x; i < n; i += 4 * 256) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = i + u * 256;
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, j < n ? j * 16u : 0x80000000u, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc ^= v[u];
+    }
+    uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    for (int off = 32; off > 0; off >>= 1) r ^= __shfl_xor(r, off);
+    __shared__ uint32_t part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
+hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* sink,
+                              hipStream_t stream) {
+    if (!workgroups || bytes % (16ull * workgroups) || bytes / workgroups >= (uint64_t(1) << 31))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(stream_read_kernel, dim3(workgroups), dim3(256), 0, stream,
+                       static_cast<const unsigned char*>(src), bytes, sink);
     return hipGetLastError();
 }
 

@@ -4,10 +4,12 @@
 // Replaces the reference's generic GEMV family (src/gemv_lds.hip:14-168,
 // src/gemv_fused.hip:17-128, src/transforms.hpp:8-52) with one wave64 design:
 //
-//   grid (N/128, S, groups), block 256 = 4 waves.  Workgroup (c, s) owns
-//   output columns [128c, 128c+128) and input blocks [s*bps, (s+1)*bps)
-//   (16 channels each, bps a multiple of 8 so the split holds whole H128
-//   input blocks).
+//   1-D grid of 256-thread workgroups (4 waves).  Workgroup (c, s, z) owns
+//   output columns [128c, 128c+128) of group z and input blocks
+//   [s*bps, (s+1)*bps) (16 channels each, bps a multiple of 8 so the split
+//   holds whole H128 input blocks).  The grid runs split-major: every column
+//   group's split s is dispatched before any split s + 1, so the last split,
+//   which finishes a single launch, comes after all the work it waits for.
 //   * prologue: the workgroup computes the FP16 core input of its channels
 //     into LDS (one wave per 128-block); the weight loads of the prefetch
 //     ring are issued before it so their latency overlaps it;
@@ -19,8 +21,8 @@
 //   * S == 1: the workgroup applies the output stage itself.  Otherwise it
 //     writes its [rows][128] partial plane; the finishing step (a second
 //     kernel, or in a single-launch plan the workgroup of split S-1, which
-//     waits for the other planes) folds the S planes in ascending split order
-//     from +0 and applies the output stage.
+//     waits for the other splits' planes) folds the S planes in
+//     ascending split order from +0 and applies the output stage.
 //
 // Per-output accumulation order (defines the core's bits; depends on I, N,
 // K only, never on the row count):
@@ -42,18 +44,38 @@ struct GemvArgs {
     const GroupWeights* table;    // per-group weights (grouped launch) or null
     const float* x;
     float* y;
-    float* partials;              // [groups][S][rows][N]
+    float* partials;              // two-launch path: F32 planes [groups][S][rows][N]
+    FusedState state;             // single-launch path (mode 1)
     uint64_t x_row_stride, y_row_stride;
     uint64_t x_group_stride, y_group_stride;
     uint32_t I, N, rows, splits, bps;
+    uint32_t ncg, groups;         // N / 128 column groups per group; groups
     float alpha, beta;
     uint32_t mode;                // 0: partial planes only, 1: the last split finishes
+    uint32_t poll_limit;          // mode 1: finisher poll rounds before giving up (0: at once)
 };
 
 __device__ __forceinline__ GroupWeights group_weights(const GemvArgs& a, int z) {
     return a.table ? a.table[z] : a.w;
 }
 
+// Workgroup L -> column group cz = L % (groups * ncg) (cz = z * ncg + c) and
+// split s = L / (groups * ncg).  The grid holds exactly groups * ncg * S
+// workgroups.  (A layout that also kept a column group's splits on one XCD --
+// workgroup L runs on XCD L % 8 -- measured slower: the device-scope partials
+// are written through to memory either way.)
+struct GemvSlot {
+    uint32_t c, s, z, cz;
+};
+__device__ __forceinline__ GemvSlot gemv_slot(const GemvArgs& a) {
+    const uint32_t cgs = a.ncg * a.groups, L = blockIdx.x;
+    GemvSlot r;
+    r.s = L / cgs;
+    r.cz = L - r.s * cgs;
+    r.z = r.cz / a.ncg;
+    r.c = r.cz - r.z * a.ncg;
+    return r;
+}
 
 // Output-stage operands of one lane's two columns (128c + lane, +64), loaded
 // ahead of the fold so their latency overlaps the completion round trip.
@@ -81,14 +103,10 @@ __device__ __forceinline__ ColumnOperands column_operands(const GroupWeights& gw
 // `plane(s, r)` returns the pointer to the 128 values of split s, row r.
 // The splits are folded in ascending order from +0; all their loads are
 // issued before the first add (one memory round trip per kFoldBatch splits).
-template <bool COHERENT, typename Plane>
+template <typename Plane>
 __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWeights& gw, const ColumnOperands& op,
                                                float* y, int c, int splits, Plane plane) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    auto load = [](const float* p) -> float {
-        if constexpr (COHERENT) return load_coherent(p);
-        else return *p;
-    };
     for (uint32_t r = blockIdx.y * GEMV_WAVES + w; r < a.rows; r += gridDim.y * GEMV_WAVES) {
         float z0 = 0.0f, z1 = 0.0f;
         for (int s = 0; s < splits; s += kFoldBatch) {
@@ -97,8 +115,8 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
             for (int u = 0; u < kFoldBatch; ++u) {
                 if (s + u < splits) {
                     const float* p = plane(s + u, r);
-                    v0[u] = load(p + lane);
-                    v1[u] = load(p + lane + 64);
+                    v0[u] = p[lane];
+                    v1[u] = p[lane + 64];
                 }
             }
 #pragma unroll
@@ -119,71 +137,135 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
     }
 }
 
-// Single-launch completion without a counter.  The planes are dedicated to
-// the plan and hold GEMV_PLANE_EMPTY between launches; a split's plane words
-// become its partial sums as its stores land (an aligned 32-bit store is seen
-// whole or not at all).  The last split's workgroup loads the other splits'
-// words until none is EMPTY, folds them in ascending split order with its own
-// sums (in LDS, split S-1) last, finishes the output, then writes EMPTY back.
-// No partial sum can be the EMPTY pattern: FP16 operands make every NaN the
-// core produces carry 13 zero low bits, and EMPTY has none.  The poll is
-// bounded; a workgroup that gives up writes NaN outputs instead of hanging.
-constexpr uint32_t kPollLimit = 1u << 22;
+// ---------------------------------------------------------------------------
+// Single-launch completion (state layout in backend.hpp).
+//
+// Every workgroup of column group cz reads epochs[cz] when it starts; the
+// launch uses plane set epochs[cz] & 1.  Splits 0..S-2 publish their partial
+// sums into it and exit.  The workgroup of split S-1 (dispatched after them,
+// on the same XCD) re-arms the other set, loads its set's words until none is
+// EMPTY, folds them in ascending split order with its own sums (in LDS, split
+// S-1) last, finishes the output and advances epochs[cz].
+//   * An aligned 32-bit store is seen whole or not at all.  No partial sum can
+//     be the EMPTY pattern: FP16 operands make every NaN the core produces
+//     carry 13 zero low bits, and EMPTY has none.
+//   * Publication and polls are device-scope accesses (sc1): a store is
+//     written through to memory, a poll reads past the L1.
+//   * The poll is bounded: a finisher that gives up writes NaN outputs, sets
+//     GEMV_STATUS_GAVE_UP in the sticky status word and still advances the
+//     epoch; partials that land afterwards sit in a set the next launch does
+//     not read, and its finisher re-arms that set.
+//   * Its dependencies were dispatched before it and at most ncg * groups
+//     finishers exist, so the wait always ends.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t load_epoch(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-template <typename Plane>
+// Plane words of column group cz in set k: [S-1][rows][128].
+__device__ __forceinline__ float* fused_planes(const GemvArgs& a, uint32_t cz, uint32_t k) {
+    const uint64_t per_cg = uint64_t(a.splits - 1) * a.rows * 128u;
+    return a.state.planes + (uint64_t(k) * a.ncg * a.groups + cz) * per_cg;
+}
+
+// Workgroup barrier that waits only for LDS traffic: global loads issued
+// before it (the finisher's output-stage operands) stay in flight, where
+// __syncthreads would wait for them too.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// `own` holds this workgroup's [rows][128] sums (split S-1); `cur` the
+// column group's planes of this launch's set, `prev` those of the other set.
+// Wave w takes rows w, w+4 (RPW = 1 or 2 rows per wave): the loads of both
+// rows are issued in one poll round (kFoldBatch / RPW splits per round).  On CDNA a wave's stores count in the
+// same vmcnt as its loads, so the re-arm stores are issued after the polls
+// (a wait for a poll would otherwise also wait for them to be written).
+template <int RPW>
 __device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeights& gw, const ColumnOperands& op,
-                                              float* y, int c, const float* own, Plane plane) {
+                                              float* y, int c, const float* own, const float* cur, float* prev,
+                                              uint32_t epoch, uint32_t cz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int others = int(a.splits) - 1;
-    for (uint32_t r = w; r < a.rows; r += GEMV_WAVES) {
-        float z0 = 0.0f, z1 = 0.0f;
-        bool complete = true;
-        for (int s = 0; s < others; s += kFoldBatch) {
-            float v0[kFoldBatch], v1[kFoldBatch];
+    constexpr int B = kFoldBatch / RPW;
+    bool gave_up = false;
+    if (uint32_t(w) < a.rows) {
+        uint32_t rr[RPW];
+        bool live[RPW];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            rr[i] = uint32_t(w + GEMV_WAVES * i);
+            live[i] = rr[i] < a.rows;
+            if (!live[i]) rr[i] = uint32_t(w);   // a valid row again, result unused
+        }
+        float z0[RPW], z1[RPW];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) z0[i] = z1[i] = 0.0f;
+        bool complete = a.poll_limit != 0;
+        for (int s = 0; s < others && complete; s += B) {
+            float v0[RPW][B], v1[RPW][B];
             for (uint32_t spin = 0;; ++spin) {
+#pragma unroll
+                for (int i = 0; i < RPW; ++i)
+#pragma unroll
+                    for (int u = 0; u < B; ++u) {
+                        const float* p = cur + ((s + u < others ? s + u : others - 1) * a.rows + rr[i]) * 128u;
+                        v0[i][u] = load_coherent(p + lane);
+                        v1[i][u] = load_coherent(p + lane + 64);
+                    }
                 bool ready = true;
 #pragma unroll
-                for (int u = 0; u < kFoldBatch; ++u) {
-                    const float* p = plane(s + u < others ? s + u : others - 1, r);
-                    v0[u] = load_coherent(p + lane);
-                    v1[u] = load_coherent(p + lane + 64);
-                }
+                for (int i = 0; i < RPW; ++i)
 #pragma unroll
-                for (int u = 0; u < kFoldBatch; ++u)
-                    ready = ready && (s + u >= others || (__builtin_bit_cast(uint32_t, v0[u]) != GEMV_PLANE_EMPTY &&
-                                                          __builtin_bit_cast(uint32_t, v1[u]) != GEMV_PLANE_EMPTY));
+                    for (int u = 0; u < B; ++u)
+                        ready = ready && (s + u >= others ||
+                                          (__builtin_bit_cast(uint32_t, v0[i][u]) != GEMV_PLANE_EMPTY &&
+                                           __builtin_bit_cast(uint32_t, v1[i][u]) != GEMV_PLANE_EMPTY));
                 if (__all(ready)) break;
-                if (spin == kPollLimit) {
+                if (spin + 1 >= a.poll_limit) {
                     complete = false;
                     break;
                 }
-                __builtin_amdgcn_s_sleep(2);
+                __builtin_amdgcn_s_sleep(1);
             }
 #pragma unroll
-            for (int u = 0; u < kFoldBatch; ++u) {
-                if (s + u < others) {
-                    z0 = z0 + v0[u];
-                    z1 = z1 + v1[u];
+            for (int i = 0; i < RPW; ++i)
+#pragma unroll
+                for (int u = 0; u < B; ++u) {
+                    if (s + u < others) {
+                        z0[i] = z0[i] + v0[i][u];
+                        z1[i] = z1[i] + v1[i][u];
+                    }
                 }
-            }
         }
-        z0 = z0 + own[r * 128 + lane];
-        z1 = z1 + own[r * 128 + lane + 64];
-        if (!complete) z0 = z1 = __builtin_nanf("");
-        h32_wave(z0, z1);
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            z0[i] = z0[i] + own[rr[i] * 128 + lane];
+            z1[i] = z1[i] + own[rr[i] * 128 + lane + 64];
+            if (!complete) z0[i] = z1[i] = __builtin_nanf("");
+        }
+        gave_up = !complete;
+        h32_wave_multi<RPW>(z0, z1);
         const int n0 = 128 * c + lane, n1 = n0 + 64;
-        float* yr = y + r * a.y_row_stride;
-        const float o0 = output_value(z0, op.sv0, gw.bias != nullptr, op.b0, a.alpha, a.beta, yr + n0);
-        const float o1 = output_value(z1, op.sv1, gw.bias != nullptr, op.b1, a.alpha, a.beta, yr + n1);
-        *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
-        *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
-        const float empty = __builtin_bit_cast(float, GEMV_PLANE_EMPTY);
-        for (int s = 0; s < others; ++s) {
-            float* p = plane(s, r);
-            store_coherent(p + lane, empty);
-            store_coherent(p + lane + 64, empty);
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            if (!live[i]) continue;
+            float* yr = y + rr[i] * a.y_row_stride;
+            const float o0 = output_value(z0[i], op.sv0, gw.bias != nullptr, op.b0, a.alpha, a.beta, yr + n0);
+            const float o1 = output_value(z1[i], op.sv1, gw.bias != nullptr, op.b1, a.alpha, a.beta, yr + n1);
+            *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+            *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
         }
     }
+    // Re-arm the previous launch's set (no workgroup of this launch reads or
+    // writes it) and advance the epoch.
+    const float empty = __builtin_bit_cast(float, GEMV_PLANE_EMPTY);
+    const uint32_t words = uint32_t(others) * a.rows * 128u;
+    for (uint32_t i = threadIdx.x; i < words; i += GEMV_THREADS) store_coherent(prev + i, empty);
+    if (gave_up && lane == 0)
+        __hip_atomic_fetch_or(a.state.status, GEMV_STATUS_GAVE_UP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.state.epochs + cz, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The block activations of every row, read from LDS ahead of the decode (up
@@ -254,7 +336,8 @@ template <int K, int CB, int RT>
 __global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu<K, RT>())))
 void gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int c = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
+    const GemvSlot place = gemv_slot(a);
+    const int c = int(place.c), s = int(place.s), z = int(place.z);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int jt = lane >> 3, g = lane & 7;
     const GroupWeights gw = group_weights(a, z);
@@ -281,6 +364,14 @@ void gemv_kernel(GemvArgs a) {
     auto block_off = [&](int t) -> uint32_t {
         return t < nb ? (w + GEMV_WAVES * t) * row_bytes + lane_off : kOutOfRange;
     };
+    // The launch's epoch (single launch with splits): issued first, so its
+    // round trip overlaps the prologue.  The finisher (S == 1, or in a single
+    // launch the workgroup of the last split) keeps its own sums in LDS;
+    // every other split publishes a plane.
+    const bool fused = a.mode == 1 && a.splits > 1;
+    const bool finisher = a.splits == 1 || (fused && uint32_t(s) == a.splits - 1);
+    const uint32_t epoch = fused ? load_epoch(a.state.epochs + place.cz) : 0u;
+
     // Prologue: FP16 core input of this split's channels, one 128-block unit
     // per wave.  The first two units' loads are issued before the weight
     // prefetch, so waiting for them does not wait for the weights.
@@ -301,10 +392,6 @@ void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) load_chunk(ring[u], rsrc, block_off(u));
 
-    // Decode the first two blocks before the prologue's arithmetic and barrier:
-    // this VALU work overlaps the latency of the input-stage loads (which
-    // queue behind the weight traffic of the whole grid) and of the other
-    // waves' H128 shuffles.  Their slots are refilled with blocks 4 and 5.
     // The chunks stay in their registers across the input stage: decoding
     // blocks ahead of the barrier (to overlap the input loads) was measured
     // slower, the decoded weights holding 32 more VGPRs per lane.
@@ -348,11 +435,9 @@ void gemv_kernel(GemvArgs a) {
         red[(w * RT + r) * 128 + 16 * jt + g] = acc[r][0];
         red[(w * RT + r) * 128 + 16 * jt + g + 8] = acc[r][1];
     }
-    __syncthreads();
+    lds_barrier();
+    float* cur = fused ? fused_planes(a, place.cz, epoch & 1u) : nullptr;
     float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
-    // The single-launch finisher (mode 1) is the workgroup of the last split:
-    // it keeps its own sums in LDS; every other split publishes a plane.
-    const bool finisher = a.splits == 1 || (a.mode == 1 && uint32_t(s) == a.splits - 1);
     for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
         const int r = idx >> 7, n = idx & 127;
         float v = red[(0 * RT + r) * 128 + n];
@@ -361,19 +446,24 @@ void gemv_kernel(GemvArgs a) {
         if (finisher) {
             red[r * 128 + n] = v;
         } else if (uint32_t(r) < a.rows) {
-            store_coherent(plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c + n, v);
+            if (fused)
+                store_coherent(cur + (uint64_t(s) * a.rows + r) * 128u + n, v);
+            else
+                *(__attribute__((address_space(1))) float*)(plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c + n) = v;
         }
     }
     if (!finisher) return;
+    // Loading the output-stage operands in the prologue instead keeps them
+    // live across the main loop and made the 1-row kernel spill (slower).
     const ColumnOperands op = column_operands(gw, c);
-    __syncthreads();
+    lds_barrier();
     if (a.splits == 1) {
-        finish_columns<false>(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
+        finish_columns(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
         return;
     }
-    finish_polled(a, gw, op, y, c, red, [&](int ss, int r) -> float* {
-        return plane_base + (uint64_t(ss) * a.rows + r) * a.N + 128 * c;
-    });
+    finish_polled<(RT + GEMV_WAVES - 1) / GEMV_WAVES>(a, gw, op, y, c, red, cur,
+                                                       fused_planes(a, place.cz, (epoch & 1u) ^ 1u), epoch,
+                                                       place.cz);
 }
 
 // Second launch of the two-kernel path: fold + output stage per column group.

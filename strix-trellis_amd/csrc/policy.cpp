@@ -37,9 +37,26 @@ uint64_t gemv_workspace_bytes(const DeviceWeights& w, uint32_t rows) {
     return align256(uint64_t(sh.splits) * rows * w.output * sizeof(float));
 }
 
-uint64_t gemv_plane_words(const DeviceWeights& w, uint64_t rows) {
+// Single-launch state: [status][epochs: groups * N/128 u32][2 plane sets].
+static uint64_t fused_epochs_offset() { return 256; }
+uint64_t fused_planes_offset(const DeviceWeights& w, uint32_t groups) {
+    return align256(fused_epochs_offset() + uint64_t(groups) * (w.output / 128) * 4);
+}
+
+uint64_t fused_state_bytes(const DeviceWeights& w, uint64_t rows, uint32_t groups) {
     const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
-    return sh.splits > 1 ? uint64_t(sh.splits) * rows * w.output : 0;
+    if (sh.splits <= 1 || !rows || !groups) return 0;
+    const uint64_t words = 2 * uint64_t(groups) * (sh.splits - 1) * rows * w.output;
+    return fused_planes_offset(w, groups) + align256(words * 4);
+}
+
+FusedState fused_state_at(void* base, const DeviceWeights& w, uint64_t /*rows*/, uint32_t groups) {
+    char* b = static_cast<char*>(base);
+    FusedState st;
+    st.status = reinterpret_cast<uint32_t*>(b);
+    st.epochs = reinterpret_cast<uint32_t*>(b + fused_epochs_offset());
+    st.planes = reinterpret_cast<float*>(b + fused_planes_offset(w, groups));
+    return st;
 }
 
 // Rows per GEMM pass: the fragment buffer of one pass stays below 1 GiB so

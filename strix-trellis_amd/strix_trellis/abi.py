@@ -184,6 +184,10 @@ _PROTOTYPES = {
     "strix_amd_gemm_splits": (_S, [vp, u64, C.POINTER(u32)]),
     "strix_amd_swiglu": (_S, [vp, vp, vp, vp, u64, C.POINTER(Stream)]),
     "strix_amd_set_gemm_handoff": (_S, [vp, u32]),
+    "strix_amd_set_gemv_poll_limit": (_S, [vp, u32]),
+    "strix_amd_plan_status": (_S, [vp, u32, C.POINTER(u32)]),
+    "strix_amd_grouped_plan_status": (_S, [vp, u32, C.POINTER(u32)]),
+    "strix_amd_stream_read": (_S, [vp, vp, u64, u32, vp, C.POINTER(Stream)]),
     "strix_tp_dense_plan_create": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), C.POINTER(vp)]),
     "strix_tp_dense_plan_create_tiled": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), u32, C.POINTER(vp)]),
     "strix_tp_dense_plan_create_splitk": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), u32, u32,
@@ -203,6 +207,9 @@ _PROTOTYPES = {
     "strix_tp_swiglu_plan_submit": (_S, [vp]),
     "strix_tp_swiglu_plan_destroy": (_S, [vp]),
 }
+
+GEMV_POLL_DEFAULT = 1 << 22
+GEMV_GAVE_UP = 1
 
 _lib = None
 

@@ -62,6 +62,10 @@ class Context:
         self.handle = h
         self.device = device
 
+    def set_gemv_poll_limit(self, limit=abi.GEMV_POLL_DEFAULT):
+        """Poll rounds of single-launch GEMV finishers on later submissions (0: give up at once)."""
+        abi.check(self.lib.strix_amd_set_gemv_poll_limit(self.handle, int(limit)), "strix_amd_set_gemv_poll_limit")
+
     def close(self):
         if self.handle:
             abi.check(self.lib.strix_context_destroy(self.handle), "strix_context_destroy")
@@ -231,9 +235,18 @@ def alloc_workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
+def _on_stream(t, stream):
+    """Tell torch's caching allocator that `t` is used on `stream` (when that is
+    not the current stream), so its memory is not reused before the work
+    enqueued there has finished."""
+    if stream is not None and stream != _t().cuda.current_stream(t.device):
+        t.record_stream(stream)
+    return t
+
+
 def _call(fn, weights, x, y, alpha, beta, workspace, stream, rank):
     if workspace is None:
-        workspace = alloc_workspace(workspace_bytes(weights, x, y, rank), x.device)
+        workspace = _on_stream(alloc_workspace(workspace_bytes(weights, x, y, rank), x.device), stream)
     d = matmul_desc(weights, x, y, alpha, beta, workspace, rank)
     abi.check(fn(weights.ctx.handle, C.byref(d), C.byref(stream_desc(stream))), fn.__name__)
     return y
@@ -251,7 +264,7 @@ class LinearPlan:
     def __init__(self, weights, x, y, alpha=1.0, beta=0.0, workspace=None, stream=None, operation="gemv"):
         self.lib = weights.lib
         if workspace is None:
-            workspace = alloc_workspace(workspace_bytes(weights, x, y), x.device)
+            workspace = _on_stream(alloc_workspace(workspace_bytes(weights, x, y), x.device), stream)
         self._keep = (weights, x, y, workspace)
         d = matmul_desc(weights, x, y, alpha, beta, workspace)
         op = abi.OPERATION_GEMV if operation == "gemv" else abi.OPERATION_GEMM
@@ -267,6 +280,12 @@ class LinearPlan:
         n = C.c_uint32()
         abi.check(self.lib.strix_amd_plan_launches(self.handle, C.byref(n)))
         return n.value
+
+    def status(self, clear=False):
+        """Sticky status flags of a single-launch plan (abi.GEMV_GAVE_UP); synchronises its stream."""
+        f = C.c_uint32()
+        abi.check(self.lib.strix_amd_plan_status(self.handle, int(bool(clear)), C.byref(f)), "strix_amd_plan_status")
+        return f.value
 
     def destroy(self):
         if self.handle:
@@ -290,7 +309,7 @@ class GroupedGemvPlan:
         abi.check(self.lib.strix_grouped_gemv_workspace_bytes(ctx.handle, C.byref(d), C.byref(need)),
                   "strix_grouped_gemv_workspace_bytes")
         if workspace is None:
-            workspace = alloc_workspace(need.value, x.device)
+            workspace = _on_stream(alloc_workspace(need.value, x.device), stream)
         d.workspace = C.c_void_p(workspace.data_ptr())
         d.workspace_bytes = workspace.numel()
         self._keep = (weights_list, x, y, workspace, handles)
@@ -301,6 +320,13 @@ class GroupedGemvPlan:
 
     def submit(self):
         abi.check(self.lib.strix_grouped_gemv_plan_submit(self.handle), "strix_grouped_gemv_plan_submit")
+
+    def status(self, clear=False):
+        """Sticky status flags (abi.GEMV_GAVE_UP); synchronises the plan's stream."""
+        f = C.c_uint32()
+        abi.check(self.lib.strix_amd_grouped_plan_status(self.handle, int(bool(clear)), C.byref(f)),
+                  "strix_amd_grouped_plan_status")
+        return f.value
 
     def destroy(self):
         if self.handle:
@@ -365,7 +391,7 @@ class MoePlan:
             k = device_ids.numel() // rows
         H = experts[0][0].output
         if workspace is None:
-            workspace = torch.empty(rows * k * H, dtype=torch.float32, device=x.device)
+            workspace = _on_stream(torch.empty(rows * k * H, dtype=torch.float32, device=x.device), stream)
         d.workspace = C.c_void_p(workspace.data_ptr())
         d.workspace_bytes = workspace.numel() * workspace.element_size()
         keep.append(workspace)
@@ -393,6 +419,14 @@ class MoePlan:
         if self.handle:
             abi.check(self.lib.strix_tp_moe_plan_destroy(self.handle), "strix_tp_moe_plan_destroy")
             self.handle = None
+
+
+def stream_read(ctx, src, nbytes, workgroups, sink, stream=None):
+    """Launch the call-floor kernel: `workgroups` x 256 threads read nbytes of
+    device tensor `src` once; one word per workgroup goes to int32 tensor `sink`."""
+    abi.check(ctx.lib.strix_amd_stream_read(ctx.handle, C.c_void_p(src.data_ptr()), int(nbytes), int(workgroups),
+                                            C.c_void_p(sink.data_ptr()), C.byref(stream_desc(stream))),
+              "strix_amd_stream_read")
 
 
 def swiglu(ctx, gate, up, stream=None):

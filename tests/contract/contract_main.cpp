@@ -411,7 +411,7 @@ static void direct_calls(strix_context c, hipStream_t hs) {
     STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &bad), STRIX_ERROR_OUT_OF_MEMORY);
     CHECK(bad == nullptr && fake::live.size() == live1);
     fake::reset_failures();
-    fake::launch_fail_at = 0;   // the EMPTY fill
+    fake::launch_fail_at = 0;   // the first fill of the single-launch state
     STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &bad), STRIX_ERROR_BACKEND);
     CHECK(bad == nullptr && fake::live.size() == live1);
     fake::reset_failures();
@@ -563,7 +563,9 @@ static void policy_rules() {
             w.bits = 4;
             for (uint32_t rows = 1; rows <= 8; ++rows) {
                 const uint64_t ws = stx::gemv_workspace_bytes(w, rows);
-                CHECK(ws % 256 == 0 && ws >= stx::gemv_plane_words(w, rows) * 4);
+                CHECK(ws % 256 == 0 && ws >= uint64_t(sh.splits > 1 ? sh.splits : 0) * rows * N * 4);
+                const uint64_t fs = stx::fused_state_bytes(w, rows, 1);
+                CHECK(sh.splits > 1 ? fs >= 2 * uint64_t(sh.splits - 1) * rows * N * 4 + 256 + (N / 128) * 4 : fs == 0);
                 CHECK(stx::linear_workspace_bytes(w, rows) >= ws);
             }
             // GEMM: the narrow split halves whole 128-channel stages; a wide

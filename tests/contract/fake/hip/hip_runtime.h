@@ -22,7 +22,7 @@ typedef ihipStream_t* hipStream_t;
 typedef int hipDevice_t;
 typedef void* hipDeviceptr_t;
 
-enum hipMemcpyKind { hipMemcpyHostToDevice = 1 };
+enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2 };
 enum hipMemoryType { hipMemoryTypeHost = 0, hipMemoryTypeDevice = 1 };
 
 struct hipDeviceProp_t {

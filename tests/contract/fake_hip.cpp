@@ -155,10 +155,11 @@ hipError_t hipFree(void* p) {
     return hipSuccess;
 }
 
-hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKind, hipStream_t) {
+hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, hipStream_t) {
     ++n.copies;
     if (trips(copy_fail_at)) return copy_error;
-    if (!in_live_block(dst, bytes)) std::abort();   // copy outside a device allocation
+    // the device side of the copy lies in a device allocation
+    if (!in_live_block(kind == hipMemcpyDeviceToHost ? src : dst, bytes)) std::abort();
     std::memcpy(dst, src, bytes);
     return hipSuccess;
 }

@@ -1,7 +1,7 @@
 // Fake kernel launchers.  Each records its call, checks that every device
 // buffer the real kernels would touch lies inside a live fake allocation of
-// sufficient size (and, for the single-launch GEMV, that its partial planes
-// arrive EMPTY-filled), and returns the injected launch result.  A failed
+// sufficient size (and, for the single-launch GEMV, that its state arrives
+// zero-filled), and returns the injected launch result.  A failed
 // check aborts: it is a contract violation of the API layer.
 #include "fake.hpp"
 #include "backend.hpp"
@@ -54,13 +54,25 @@ hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& c, hipStream_t 
     return fake::launch_result();
 }
 
-hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& c, float* planes, hipStream_t s) {
+// The single-launch state of `groups` groups starts at st.status, lies in
+// device memory and holds what a fresh plan holds (no launch ran): status and
+// epochs 0, every plane word EMPTY.
+void check_state(const DeviceWeights& w, uint64_t rows, uint32_t groups, const FusedState& st, const char* who) {
+    const uint64_t bytes = fused_state_bytes(w, rows, groups);
+    require(bytes > 0, "single launch without split partials", who);
+    require(fake::in_live_block(st.status, bytes), "single-launch state outside device memory", who);
+    const FusedState at = fused_state_at(st.status, w, rows, groups);
+    require(at.epochs == st.epochs && at.planes == st.planes, "single-launch state layout", who);
+    const uint64_t planes = fused_planes_offset(w, groups) / 4;
+    const uint32_t* p = st.status;
+    for (uint64_t i = 0; i < bytes / 4; ++i)
+        require(p[i] == (i < planes ? 0u : GEMV_PLANE_EMPTY), "single-launch state not initialised", who);
+}
+
+hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& c, const FusedState& st, hipStream_t s) {
     check_call(w, c, "launch_gemv_fused");
-    const uint64_t words = gemv_plane_words(w, c.rows);
-    require(fake::in_live_block(planes, words * 4), "partial planes outside device memory", "launch_gemv_fused");
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(planes);
-    for (uint64_t i = 0; i < words; ++i) require(p[i] == GEMV_PLANE_EMPTY, "planes not EMPTY on entry", "launch_gemv_fused");
-    record("gemv_fused", c.rows, c.workspace, planes, s, c.alpha, c.beta);
+    check_state(w, c.rows, 1, st, "launch_gemv_fused");
+    record("gemv_fused", c.rows, c.workspace, st.planes, s, c.alpha, c.beta);
     return fake::launch_result();
 }
 
@@ -75,7 +87,8 @@ hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& c, cons
 
 hipError_t launch_gemv_grouped(const DeviceWeights& g, const GroupWeights* table, uint32_t groups,
                                const LinearCall& c, uint64_t x_group_stride, uint64_t y_group_stride,
-                               bool single_launch, hipStream_t s) {
+                               const FusedState* st, hipStream_t s) {
+    const bool single_launch = st != nullptr;
     require(groups > 0, "no groups", "launch_gemv_grouped");
     require(fake::in_live_block(table, groups * sizeof(GroupWeights)), "group table outside device memory",
             "launch_gemv_grouped");
@@ -83,14 +96,7 @@ hipError_t launch_gemv_grouped(const DeviceWeights& g, const GroupWeights* table
     const uint64_t yb = ((groups - 1) * y_group_stride + (c.rows - 1) * c.y_row_stride + g.output) * 4;
     require(fake::in_live_block(c.x, xb), "grouped input outside device memory", "launch_gemv_grouped");
     require(fake::in_live_block(c.y, yb), "grouped output outside device memory", "launch_gemv_grouped");
-    if (single_launch) {
-        const uint64_t words = uint64_t(groups) * gemv_plane_words(g, c.rows);
-        require(fake::in_live_block(c.workspace, words * 4), "grouped planes outside device memory",
-                "launch_gemv_grouped");
-        const uint32_t* p = static_cast<const uint32_t*>(c.workspace);
-        for (uint64_t i = 0; i < words; ++i)
-            require(p[i] == GEMV_PLANE_EMPTY, "grouped planes not EMPTY on entry", "launch_gemv_grouped");
-    }
+    if (single_launch) check_state(g, c.rows, groups, *st, "launch_gemv_grouped");
     record(single_launch ? "gemv_grouped_fused" : "gemv_grouped", c.rows, c.workspace, nullptr, s, c.alpha, c.beta);
     return fake::launch_result();
 }
@@ -132,6 +138,16 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStrea
     if (e == hipSuccess)
         for (uint64_t i = 0; i < count; ++i) p[i] = value;
     return e;
+}
+
+hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* sink,
+                              hipStream_t s) {
+    require(workgroups > 0 && bytes % (16ull * workgroups) == 0, "stream read shape", "launch_stream_read");
+    require(fake::in_live_block(src, bytes), "stream read source outside device memory", "launch_stream_read");
+    require(fake::in_live_block(sink, uint64_t(workgroups) * 4), "stream read sink outside device memory",
+            "launch_stream_read");
+    record("stream_read", 0, nullptr, nullptr, s, 0, 0);
+    return fake::launch_result();
 }
 
 static void check_moe(const MoeArgs& a, bool gate_up, const char* who) {

@@ -28,14 +28,24 @@ def activations(R, I, seed):
     return rng(seed).standard_normal((R, I)).astype(np.float16).astype(np.float32)
 
 
+def gate_values(actual, reference):
+    """(maxabs, nrmse) of an output against its reference; inf when not all finite."""
+    a = np.asarray(actual, dtype=np.float64)
+    r = np.asarray(reference, dtype=np.float64)
+    if not np.isfinite(a).all():
+        return float("inf"), float("inf")
+    maxabs = float(np.max(np.abs(a - r))) if a.size else 0.0
+    nrmse = float(np.sqrt(np.sum((a - r) ** 2) / max(np.sum(r ** 2), 1e-30)))
+    return maxabs, nrmse
+
+
 def gate(actual, reference):
     """Acceptance of a full operator output (reference docs/GPU_TESTS.md:124-143):
     maxabs <= 5e-4 * max(1, max|ref|) and nrmse <= 3e-5, all finite."""
     a = np.asarray(actual, dtype=np.float64)
     r = np.asarray(reference, dtype=np.float64)
     assert np.isfinite(a).all(), "nonfinite output"
-    maxabs = float(np.max(np.abs(a - r))) if a.size else 0.0
-    nrmse = float(np.sqrt(np.sum((a - r) ** 2) / max(np.sum(r ** 2), 1e-30)))
+    maxabs, nrmse = gate_values(a, r)
     limit = 5e-4 * max(1.0, float(np.max(np.abs(r))) if r.size else 1.0)
     assert maxabs <= limit, f"maxabs {maxabs:.3e} > {limit:.3e}"
     assert nrmse <= 3e-5, f"nrmse {nrmse:.3e} > 3e-5"

@@ -14,7 +14,7 @@ is built).  The driver ``tests/contract/contract_main.cpp`` checks:
 - plan submission allocates, copies, synchronises and queries nothing
   (reference docs/API.md:230-295);
 - every launcher receives device buffers sized by its own policy, and the
-  single-launch GEMV receives EMPTY-filled partial planes;
+  single-launch GEMV receives an initialised state;
 - the decomposition policy (GEMV splits, GEMM passes, K splits, tile widths,
   handoff, MoE splits) covers every layer of a sweep of shapes within the
   kernels' limits and follows its documented choice rules.
