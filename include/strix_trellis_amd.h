@@ -91,6 +91,23 @@ strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan plan, uint32_
 strix_status strix_amd_stream_read(strix_context context, const void *src, uint64_t bytes, uint32_t workgroups,
     uint32_t *sink, const strix_stream *stream);
 
+/* strix_gemv for 1-8 rows that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The
+ * descriptor is validated as for strix_gemv, but must carry no workspace
+ * (workspace NULL, workspace_bytes 0): the GEMV's split partial planes go to a
+ * static device array of STRIX_AMD_GEMV_NOALLOC_SCRATCH_BYTES that the library
+ * holds on every device it runs on until the process ends.  A layer whose
+ * planes (splits x rows x N floats) exceed it is rejected with
+ * STRIX_ERROR_INSUFFICIENT_BUFFER; more than 8 rows with
+ * STRIX_ERROR_UNSUPPORTED_FORMAT.  The output has strix_gemv's exact bits.
+ * Every call on a device shares that device's array: calls that overlap in
+ * time on one device (different streams, or graphs replayed concurrently)
+ * race and must be ordered by the caller. */
+#define STRIX_AMD_GEMV_NOALLOC_SCRATCH_BYTES 4194304u
+strix_status strix_amd_gemv_noalloc(strix_context context, const strix_matmul_desc *desc,
+    const strix_stream *stream);
+
 #ifdef __cplusplus
 }
 #endif

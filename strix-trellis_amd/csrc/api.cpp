@@ -418,8 +418,14 @@ strix_status strix_context_create(const strix_context_desc* d, strix_context* ou
     if (e == hipErrorInvalidDevice || e == hipErrorNoDevice) return STRIX_ERROR_UNSUPPORTED_DEVICE;
     if (e != hipSuccess) return from_hip(e);
     if (!is_gfx950(props)) return STRIX_ERROR_UNSUPPORTED_DEVICE;
+    // The allocation-free GEMV's scratch address on this device (looked up
+    // once per device; no allocation).
+    void* scratch = nullptr;
+    const hipError_t se = stx::gemv_scratch_address(d->device_ordinal, &scratch);
+    if (se != hipSuccess) return from_hip(se);
     auto* c = new (std::nothrow) strix_context_impl;
     if (!c) return STRIX_ERROR_OUT_OF_MEMORY;
+    c->gemv_scratch = scratch;
     c->device = d->device_ordinal;
     c->compute_units = props.multiProcessorCount;
     *out = c;

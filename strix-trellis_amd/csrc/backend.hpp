@@ -119,6 +119,13 @@ hipError_t launch_input_stage(const DeviceWeights& w, const float* x, uint64_t r
 hipError_t launch_output_stage(const DeviceWeights& w, const float* core, uint64_t rows, float* y,
                                float alpha, float beta, hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStream_t stream);
+// Allocation-free GEMV (strix_amd_gemv_noalloc): the split partial planes of
+// the two-launch GEMV in a static device array of kGemvScratchBytes per
+// device (noalloc.hip).  gemv_scratch_address returns that array's address on
+// `device`, looked up once per device with the device current.
+constexpr uint64_t kGemvScratchBytes = uint64_t(4) << 20;
+hipError_t gemv_scratch_address(int device, void** out);
+
 // Streaming read of `bytes` (a multiple of 16) by `workgroups` x 256 threads,
 // 16-byte loads, nothing stored but one word per workgroup into sink: the
 // measured call floor of a kernel that reads that many bytes once.

@@ -260,6 +260,15 @@ def gemm(weights, x, y, alpha=1.0, beta=0.0, workspace=None, stream=None):
     return _call(weights.lib.strix_gemm, weights, x, y, alpha, beta, workspace, stream, None)
 
 
+def gemv_noalloc(weights, x, y, alpha=1.0, beta=0.0, stream=None):
+    """strix_amd_gemv_noalloc: strix_gemv for 1-8 rows with no workspace and no
+    allocation (the split planes use the library's static device scratch)."""
+    d = matmul_desc(weights, x, y, alpha, beta, None)
+    abi.check(weights.lib.strix_amd_gemv_noalloc(weights.ctx.handle, C.byref(d), C.byref(stream_desc(stream))),
+              "strix_amd_gemv_noalloc")
+    return y
+
+
 class LinearPlan:
     def __init__(self, weights, x, y, alpha=1.0, beta=0.0, workspace=None, stream=None, operation="gemv"):
         self.lib = weights.lib

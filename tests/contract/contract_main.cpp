@@ -605,6 +605,78 @@ static void policy_rules() {
         }
 }
 
+// Allocation-free GEMV: no allocation, free, copy or synchronisation; the
+// planes go to the device's static scratch; the workspace fields must be
+// empty; more than 8 rows and planes beyond the scratch are rejected.
+static void noalloc_calls(strix_context c, hipStream_t hs) {
+    Dense d{HostLinear(1024, 2048, 4, false)};
+    strix_stream st = stream_of(hs);
+    const strix_exl3_parts_desc parts = d.host.parts();
+    STATUS(strix_weights_prepare_parts(c, &parts, &st, &d.w), STRIX_SUCCESS);
+    d.x = device_alloc(9 * d.host.columns * 4);
+    d.y = device_alloc(9 * d.host.rows * 4);
+    void* scratch = nullptr;
+    CHECK(stx::gemv_scratch_address(0, &scratch) == hipSuccess && scratch);
+    uint32_t bps = 0, splits = 0;
+    STATUS(strix_amd_gemv_shape(d.w, &bps, &splits), STRIX_SUCCESS);
+    CHECK(splits > 1);
+    for (uint64_t rows : {8u, 3u, 1u}) {
+        strix_matmul_desc m = matmul(d, rows, 2);
+        m.workspace = nullptr;
+        m.workspace_bytes = 0;
+        fake::launches.clear();
+        const fake::Counters before = fake::n;
+        STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_SUCCESS);
+        CHECK(fake::n.mallocs == before.mallocs && fake::n.frees == before.frees);
+        CHECK(fake::n.copies == before.copies && fake::n.syncs == before.syncs);
+        CHECK(fake::launches.size() == 1 && fake::launches[0].name == "gemv");
+        CHECK(fake::launches[0].workspace == scratch && fake::launches[0].rows == rows);
+    }
+    strix_matmul_desc m = matmul(d, 2, 2);   // a workspace is not accepted
+    void* ws = device_alloc(1 << 20);
+    m.workspace = ws;
+    m.workspace_bytes = 1 << 20;
+    STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    m.workspace = nullptr;
+    STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    CHECK(hipFree(ws) == hipSuccess);
+    m = matmul(d, 9, 2);
+    m.workspace = nullptr;
+    m.workspace_bytes = 0;
+    STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_ERROR_UNSUPPORTED_FORMAT);
+    m = matmul(d, 0, 2);
+    m.workspace = nullptr;
+    m.workspace_bytes = 0;
+    fake::launches.clear();
+    STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_SUCCESS);
+    CHECK(fake::launches.empty());
+    fake::launch_fail_at = 0;
+    m = matmul(d, 1, 2);
+    m.workspace = nullptr;
+    m.workspace_bytes = 0;
+    STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_ERROR_BACKEND);
+    fake::reset_failures();
+    STATUS(strix_weights_destroy(d.w), STRIX_SUCCESS);
+    // 5120 -> 40960: four splits, so 8 rows need 5.2 MB of planes (> 4 MiB).
+    Dense big{HostLinear(40960, 5120, 1, false)};
+    const strix_exl3_parts_desc bp = big.host.parts();
+    STATUS(strix_weights_prepare_parts(c, &bp, &st, &big.w), STRIX_SUCCESS);
+    STATUS(strix_amd_gemv_shape(big.w, &bps, &splits), STRIX_SUCCESS);
+    CHECK(uint64_t(splits) * 8 * 40960 * 4 > stx::kGemvScratchBytes);
+    big.x = device_alloc(8 * big.host.columns * 4);
+    big.y = device_alloc(8 * big.host.rows * 4);
+    m = matmul(big, 8, 2);
+    m.workspace = nullptr;
+    m.workspace_bytes = 0;
+    STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_ERROR_INSUFFICIENT_BUFFER);
+    m = matmul(big, 2, 2);   // two rows fit
+    m.workspace = nullptr;
+    m.workspace_bytes = 0;
+    STATUS(strix_amd_gemv_noalloc(c, &m, &st), STRIX_SUCCESS);
+    STATUS(strix_weights_destroy(big.w), STRIX_SUCCESS);
+    for (void* p : {d.x, d.y, big.x, big.y}) CHECK(hipFree(p) == hipSuccess);
+}
+
 int main() {
     policy_rules();
     context_rules();
@@ -615,6 +687,7 @@ int main() {
     prepare_failures(c, hs);
     direct_calls(c, hs);
     moe_plan(c, hs);
+    noalloc_calls(c, hs);
     // The default stream (NULL) is accepted everywhere a stream is.
     {
         const HostLinear L(128, 128, 2, false);
@@ -625,7 +698,10 @@ int main() {
         STATUS(strix_weights_destroy(w), STRIX_SUCCESS);
     }
     STATUS(strix_context_destroy(c), STRIX_SUCCESS);
-    CHECK(fake::live.empty());
+    // Only the static scratch of the allocation-free GEMV remains.
+    void* scratch = nullptr;
+    CHECK(stx::gemv_scratch_address(0, &scratch) == hipSuccess);
+    CHECK(fake::live.size() == 1 && fake::live.count(reinterpret_cast<uintptr_t>(scratch)) == 1);
     fake::destroy_streams();
     std::printf("contract: %d checks passed\n", checks);
     return 0;

@@ -9,6 +9,8 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <map>
+#include <vector>
 
 namespace {
 
@@ -138,6 +140,19 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStrea
     if (e == hipSuccess)
         for (uint64_t i = 0; i < count; ++i) p[i] = value;
     return e;
+}
+
+// The static scratch of the allocation-free GEMV: one host block per fake
+// device, registered as a live device block once (not a hipMalloc).
+hipError_t gemv_scratch_address(int device, void** out) {
+    static std::map<int, std::vector<unsigned char>> blocks;
+    auto it = blocks.find(device);
+    if (it == blocks.end()) {
+        it = blocks.emplace(device, std::vector<unsigned char>(kGemvScratchBytes)).first;
+        fake::live[reinterpret_cast<uintptr_t>(it->second.data())] = fake::Block{kGemvScratchBytes, device};
+    }
+    *out = it->second.data();
+    return hipSuccess;
 }
 
 hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* sink,

@@ -29,7 +29,7 @@ import pytest
 ROOT = Path(__file__).resolve().parents[1]
 CSRC = ROOT / "strix-trellis_amd" / "csrc"
 CONTRACT = ROOT / "tests" / "contract"
-HOST_SOURCES = ["api.cpp", "api_grouped.cpp", "api_moe.cpp", "api_tp.cpp", "dispatch.cpp", "policy.cpp"]
+HOST_SOURCES = sorted(p.name for p in CSRC.glob("api*.cpp")) + ["dispatch.cpp", "policy.cpp"]
 FAKE_SOURCES = ["fake_hip.cpp", "fake_launch.cpp", "contract_main.cpp"]
 
 
