@@ -8,7 +8,8 @@ over a cold rotation of >= 1 GiB of distinct weight copies (more than 4x the
 Also reported on the same JSON line:
   sweep_gemv     decode GEMV, R = 1, 2, 4, 8 x {5120^2, 4096 -> 12288} x K4-6
   sweep_gemm     prefill GEMM, M = 128, 512, 2048 x the same shapes x K4-6
-  grouped_o_a    16 groups x (4096 -> 1024) K5, R = 1..8, one grouped plan
+  grouped_o_a    16 groups x (4096 -> 1024) K5, R = 1..8, the split and the
+                 owner-fold grouped plan (cells carry "fold")
   moe_k2         64 experts (4096 <-> 1536, K2), 8 tokens, top-8, device routes
   roofline       the headline kernel: packed bytes / its mean launch time
   fp16_library   per GEMV/GEMM cell: the same product on dense FP16 weights
@@ -68,7 +69,7 @@ class Rotation:
     number of passes y holds the result of one call.
     """
 
-    def __init__(self, ctx, I, N, K, R, seed, op="gemv", groups=1, min_bytes=ROTATION_BYTES):
+    def __init__(self, ctx, I, N, K, R, seed, op="gemv", groups=1, min_bytes=ROTATION_BYTES, fold=None):
         import torch
         import synth
         from strix_trellis import runtime
@@ -87,8 +88,15 @@ class Rotation:
             self.weights.extend(wl)
             if op == "grouped":
                 # a grouped plan keeps its weight table in its own workspace
-                plan = runtime.GroupedGemvPlan(wl, self.x, self.y, R, igs=I, ogs=N, irs=groups * I,
-                                               ors=groups * N, stream=self.stream)
+                if fold is not None:
+                    ctx.set_grouped_fold(fold)
+                try:
+                    plan = runtime.GroupedGemvPlan(wl, self.x, self.y, R, igs=I, ogs=N, irs=groups * I,
+                                                   ors=groups * N, stream=self.stream)
+                finally:
+                    if fold is not None:
+                        ctx.set_grouped_fold(0)
+                self.fold = plan.fold()
             else:
                 if ws is None:
                     ws = runtime.alloc_workspace(runtime.workspace_bytes(wl[0], self.x, self.y), "cuda:0")
@@ -340,15 +348,17 @@ def bench_gemm(ctx, M, I, N, K, steps, warmup, seed):
             "speedup_vs_fp16_library": round(lib["us"] / (t["ms"] * 1e3), 2)}
 
 
-def bench_grouped(ctx, G, I, N, K, R, steps, warmup, seed):
-    rot = Rotation(ctx, I, N, K, R, seed, "grouped", groups=G)
+def bench_grouped(ctx, G, I, N, K, R, steps, warmup, seed, fold=None):
+    """fold: None (the library's choice), 1 (split plan) or 2 (owner-fold plan)."""
+    rot = Rotation(ctx, I, N, K, R, seed, "grouped", groups=G, fold=fold)
     try:
         t = time_rotation(rot, steps, warmup)
     finally:
         rot.close()
     gbps = rot.packed / (t["ms"] * 1e-3) / 1e9
     floor = call_floor(ctx, [(rot.packed, gemv_grid(ctx, I, N, G))], steps, warmup)
-    return {"groups": G, "I": I, "N": N, "K": K, "R": R, "us": round(t["ms"] * 1e3, 3),
+    return {"groups": G, "I": I, "N": N, "K": K, "R": R, "fold": {1: "split", 2: "owner"}[rot.fold],
+            "us": round(t["ms"] * 1e3, 3),
             "packed_GBps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1),
             "call_floor_us": floor, "pct_call_floor": round(100 * floor / (t["ms"] * 1e3), 1),
             "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "replay_matches_eager": t["output_check"]}
@@ -542,7 +552,9 @@ def run_section(ctx, which, steps, warmup):
                     cells.append(bench_gemm(ctx, M, I, N, K, 48, 8, synth.BASE_SEED + 2))
     elif which == "grouped":
         for R in range(1, 9):
-            cells.append(bench_grouped(ctx, 16, 4096, 1024, 5, R, small_steps, small_warm, synth.BASE_SEED + 3))
+            for fold in (1, 2):
+                cells.append(bench_grouped(ctx, 16, 4096, 1024, 5, R, small_steps, small_warm, synth.BASE_SEED + 3,
+                                           fold))
     else:
         cells.append(bench_moe(ctx, max(64, steps // 32), max(8, warmup // 32), synth.BASE_SEED + 4))
     for c in cells:
@@ -598,9 +610,10 @@ def main():
                     log(json.dumps(cell))
                     gemm.append(cell)
         for R in range(1, 9):
-            cell = bench_grouped(ctx, 16, 4096, 1024, 5, R, small_steps, small_warm, synth.BASE_SEED + 3)
-            log(json.dumps(cell))
-            grouped.append(cell)
+            for fold in (1, 2):
+                cell = bench_grouped(ctx, 16, 4096, 1024, 5, R, small_steps, small_warm, synth.BASE_SEED + 3, fold)
+                log(json.dumps(cell))
+                grouped.append(cell)
         moe_cell = bench_moe(ctx, max(64, args.steps // 32), max(8, args.warmup // 32), synth.BASE_SEED + 4)
         log(json.dumps(moe_cell))
     cpu = None if args.no_cpu else cpu_baseline()

@@ -91,6 +91,16 @@ strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan plan, uint32_
 strix_status strix_amd_stream_read(strix_context context, const void *src, uint64_t bytes, uint32_t workgroups,
     uint32_t *sink, const strix_stream *stream);
 
+/* Grouped GEMV plans come in two folds with the same output bits: the split
+ * plan (each output group's input splits run in separate workgroups and the
+ * last one folds the others' published partials) and the owner-fold plan (one
+ * workgroup per 128-column output group runs every split and folds them
+ * itself; reference src/dense_r1_group_owner.hip).  fold: 0 = the library's
+ * choice, 1 = split, 2 = owner, for grouped plans created later on the
+ * context; strix_amd_grouped_plan_fold reports a plan's fold (1 or 2). */
+strix_status strix_amd_set_grouped_fold(strix_context context, uint32_t fold);
+strix_status strix_amd_grouped_plan_fold(strix_grouped_gemv_plan plan, uint32_t *fold);
+
 /* strix_gemv for 1-8 rows that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation).  The

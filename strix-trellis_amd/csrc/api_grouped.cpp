@@ -91,12 +91,13 @@ strix_status validate(strix_context c, const strix_grouped_gemv_desc* d, Validat
 }  // namespace
 
 struct strix_grouped_gemv_plan_impl {
-    strix_context owner = nullptr;
+    strix_context owner_ctx = nullptr;
     std::vector<strix_weights> retained;
     stx::DeviceWeights geometry{};
     stx::LinearCall call{};
     const stx::GroupWeights* table = nullptr;
     stx::FusedState fused{};   // null when one split suffices
+    bool owner = false;        // owner-fold plan (no planes) instead of the split plan
     uint64_t xgs = 0, ygs = 0;
     hipStream_t stream{};
 };
@@ -161,7 +162,7 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
         delete p;
         return from_hip(e != hipSuccess ? e : done);
     }
-    p->owner = c;
+    p->owner_ctx = c;
     p->geometry = v.geometry;
     p->stream = hs;
     p->xgs = v.xgs;
@@ -176,6 +177,10 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
     p->call.workspace = nullptr;
     if (v.layout.state_bytes)
         p->fused = stx::fused_state_at(base + v.layout.state_offset, v.geometry, v.rows, uint32_t(v.weights.size()));
+    const uint32_t G = uint32_t(v.weights.size());
+    const bool want_owner = c->grouped_fold == 2 ||
+                            (c->grouped_fold == 0 && stx::grouped_owner_preferred(v.geometry, G, v.rows));
+    p->owner = want_owner && stx::gemv_owner_fits(v.geometry, v.rows);
     for (strix_weights w : v.weights) ++w->plans;
     *out = p;
     return STRIX_SUCCESS;
@@ -183,10 +188,13 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
 
 strix_status strix_grouped_gemv_plan_submit(strix_grouped_gemv_plan p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
-    const strix_status s = context_ok(p->owner);
+    const strix_status s = context_ok(p->owner_ctx);
     if (s != STRIX_SUCCESS) return s;
     stx::LinearCall call = p->call;
-    call.gemv_poll_limit = p->owner->gemv_poll_limit;
+    if (p->owner)
+        return from_hip(stx::launch_gemv_owner(p->geometry, p->table, uint32_t(p->retained.size()), call, p->xgs,
+                                               p->ygs, p->stream));
+    call.gemv_poll_limit = p->owner_ctx->gemv_poll_limit;
     const stx::FusedState* st = p->fused.planes ? &p->fused : nullptr;
     if (!st && stx::gemv_shape(p->geometry.input, p->geometry.output, p->geometry.bits).splits > 1)
         return STRIX_ERROR_BACKEND;
@@ -197,9 +205,24 @@ strix_status strix_grouped_gemv_plan_submit(strix_grouped_gemv_plan p) {
 strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan p, uint32_t clear, uint32_t* flags) {
     if (flags) *flags = 0;
     if (!p || !flags) return STRIX_ERROR_INVALID_ARGUMENT;
-    const strix_status s = context_ok(p->owner);
+    const strix_status s = context_ok(p->owner_ctx);
     if (s != STRIX_SUCCESS) return s;
     return read_fused_status(p->fused, p->stream, flags, clear);
+}
+
+strix_status strix_amd_grouped_plan_fold(strix_grouped_gemv_plan p, uint32_t* fold) {
+    if (fold) *fold = 0;
+    if (!p || !fold) return STRIX_ERROR_INVALID_ARGUMENT;
+    *fold = p->owner ? 2u : 1u;
+    return STRIX_SUCCESS;
+}
+
+strix_status strix_amd_set_grouped_fold(strix_context c, uint32_t fold) {
+    const strix_status s = context_ok(c);
+    if (s != STRIX_SUCCESS) return s;
+    if (fold > 2) return STRIX_ERROR_INVALID_ARGUMENT;
+    c->grouped_fold = fold;
+    return STRIX_SUCCESS;
 }
 
 strix_status strix_grouped_gemv_plan_destroy(strix_grouped_gemv_plan p) {

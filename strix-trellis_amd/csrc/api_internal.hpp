@@ -14,6 +14,7 @@ struct strix_context_impl {
     uint32_t gemm_handoff_poll = 4096;   // LinearCall::handoff_poll_limit of calls made on it
     uint32_t gemv_poll_limit = stx::GEMV_DEFAULT_POLL_LIMIT;   // single-launch GEMV finishers
     void* gemv_scratch = nullptr;   // this device's static scratch (strix_amd_gemv_noalloc)
+    uint32_t grouped_fold = 0;      // grouped plans created on it: 0 library's choice, 1 split, 2 owner
 };
 
 struct strix_weights_impl {

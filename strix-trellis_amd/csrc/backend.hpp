@@ -102,6 +102,16 @@ hipError_t launch_plane_finish(const DeviceWeights& w, const LinearCall& call, c
 hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
                                const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
                                const FusedState* state, hipStream_t stream);
+// Owner-fold grouped GEMV: one 16-wave workgroup per 128-column group folds
+// all of its splits itself (no partial planes, no waiting); every output has
+// the bits of launch_gemv_grouped.  gemv_owner_fits: rows 1..8, a split layer,
+// LDS within 64 KiB.
+bool gemv_owner_fits(const DeviceWeights& geometry, uint64_t rows);
+hipError_t launch_gemv_owner(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
+                             const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
+                             hipStream_t stream);
+// The library's choice between the owner-fold and the split grouped plan.
+bool grouped_owner_preferred(const DeviceWeights& geometry, uint32_t groups, uint64_t rows);
 // Prefill path (any row count): input stage to FP16 in the workspace, then the
 // MFMA core with the fused output stage.
 hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);

@@ -174,6 +174,29 @@ hipError_t launch_gemv_grouped(const DeviceWeights& geometry, const GroupWeights
     return hipGetLastError();
 }
 
+using GemvOwnerDispatch = hipError_t (*)(const GemvLaunch&);
+static const GemvOwnerDispatch owner_table[8] = {gemv_owner_dispatch<1>, gemv_owner_dispatch<2>,
+                                                 gemv_owner_dispatch<3>, gemv_owner_dispatch<4>,
+                                                 gemv_owner_dispatch<5>, gemv_owner_dispatch<6>,
+                                                 gemv_owner_dispatch<7>, gemv_owner_dispatch<8>};
+
+// The owner kernel keeps its inputs and wave partials in at most 64 KiB of LDS.
+bool gemv_owner_fits(const DeviceWeights& w, uint64_t rows) {
+    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
+    return rows >= 1 && rows <= 8 && sh.splits > 1 && owner_lds_bytes(rows_template(rows), sh.bps) <= 65536;
+}
+
+hipError_t launch_gemv_owner(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
+                             const LinearCall& call, uint64_t x_group_stride, uint64_t y_group_stride,
+                             hipStream_t stream) {
+    if (!gemv_fits(geometry, groups, call.rows) || !gemv_owner_fits(geometry, call.rows)) return hipErrorInvalidValue;
+    GemvLaunch l = make_launch(geometry, table, groups, call, x_group_stride, y_group_stride, nullptr, nullptr,
+                               stream);
+    l.grid = dim3(l.args.ncg * groups, 1, 1);
+    l.lds = owner_lds_bytes(l.rows_template, l.args.bps);
+    return owner_table[geometry.bits - 1](l);
+}
+
 // ---------------------------------------------------------------------------
 // Diagnostics and utilities.
 // ---------------------------------------------------------------------------

@@ -466,6 +466,139 @@ void gemv_kernel(GemvArgs a) {
                                                        place.cz);
 }
 
+// ---------------------------------------------------------------------------
+// Owner-fold GEMV: one 16-wave workgroup per 128-column group folds every
+// split itself, so nothing crosses workgroups (reference
+// src/dense_r1_group_owner.hip:1-10 describes the same plan for wave32).
+//
+// The workgroup is four groups of the split kernel's four waves.  Pass p runs
+// splits 4p .. 4p+3 side by side, group j taking split 4p + j exactly as a
+// split workgroup would: its input stage, its blocks (wave w of the group
+// takes blocks w, w+4, ...), its lane chains and its wave-order fold.  Thread
+// t < RT*128 owns output (row t/128, column t%128) and adds each split's
+// partial to its running sum in ascending split order from +0.  So every
+// output has the bits of the split plan (gemv_kernel), whose finisher adds
+// the same partials in the same order.
+// LDS: the groups' core inputs [4][RT][bps*16] FP16, aliased (after a barrier)
+// with the wave partials [4][4][RT][128] F32; after the last pass the row
+// sums [RT][128] F32 reuse the same space.
+// ---------------------------------------------------------------------------
+constexpr int OWNER_GROUPS = 4;
+constexpr int OWNER_THREADS = GEMV_THREADS * OWNER_GROUPS;
+
+inline size_t owner_lds_bytes(uint32_t rows_template, uint32_t bps) {
+    const size_t act = size_t(OWNER_GROUPS) * rows_template * bps * 16 * 2;
+    const size_t red = size_t(OWNER_GROUPS) * GEMV_WAVES * rows_template * 128 * 4;
+    return act > red ? act : red;
+}
+
+template <int K, int CB, int RT>
+__global__ __launch_bounds__(OWNER_THREADS) void gemv_owner_kernel(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t cz = blockIdx.x, z = cz / a.ncg, c = cz - z * a.ncg;
+    const int tid = threadIdx.x, grp = tid >> 8, w = (tid >> 6) & 3, lane = tid & 63;
+    const int jt = lane >> 3, g = lane & 7;
+    const GroupWeights gw = group_weights(a, int(z));
+    const float* x = a.x + z * a.x_group_stride;
+    float* y = a.y + z * a.y_group_stride;
+
+    constexpr uint32_t tile_bytes = 32u * K;
+    const uint32_t row_bytes = (a.N >> 4) * tile_bytes;
+    const uint32_t lane_off = (8u * c + jt) * tile_bytes + g * 4u * K;
+    const int nb = a.bps / GEMV_WAVES;
+    const uint32_t act_row = a.bps * 16;
+    _Float16* act = reinterpret_cast<_Float16*>(smem) + size_t(grp) * RT * act_row;   // [RT][bps*16]
+    float* red = reinterpret_cast<float*>(smem);                                       // [4][4][RT][128]
+    constexpr uint32_t kOutOfRange = 0x80000000u;
+    const int hblocks = a.bps / 8, units = RT * hblocks;
+    const bool first = g == 0;
+
+    float sum = 0.0f;   // thread tid < RT*128: output (tid / 128, tid % 128)
+    for (uint32_t s0 = 0; s0 < a.splits; s0 += OWNER_GROUPS) {
+        const uint32_t s = s0 + uint32_t(grp);
+        const bool active = s < a.splits;
+        float acc[RT][2];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+        Chunk<K> ring[4];
+        const uint32_t a0 = (active ? s : s0) * a.bps;
+        const auto rsrc = make_rsrc(reinterpret_cast<const char*>(gw.trellis) + uint64_t(a0) * row_bytes,
+                                    active ? a.bps * row_bytes : 0u);
+        auto block_off = [&](int t) -> uint32_t {
+            return t < nb ? (w + GEMV_WAVES * t) * row_bytes + lane_off : kOutOfRange;
+        };
+        if (active) {
+            auto unit_load = [&](int u) -> InputLoad {
+                const int r = u / hblocks, hb = u % hblocks;
+                const uint32_t ch = a0 * 16 + hb * 128;
+                const bool live = uint32_t(r) < a.rows;
+                return input_load(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, live);
+            };
+            auto unit_out = [&](int u) -> _Float16* { return act + (u / hblocks) * act_row + (u % hblocks) * 128; };
+            const InputLoad pre0 = unit_load(w < units ? w : 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) load_chunk(ring[u], rsrc, block_off(u));
+            if (w < units) input_compute(pre0, unit_out(w));
+            for (int u = w + GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
+        }
+        __syncthreads();
+        if (active) {
+            for (int t = 0; t < nb; t += 4) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    Chunk<K>& slot = ring[u];
+                    if (t + u < nb) {
+                        half2_t wq[4][4];
+                        link_chunk(slot, first);
+                        decode_chunk<K, CB>(slot, wq);
+                        dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+                    }
+                    load_chunk(slot, rsrc, block_off(t + u + 4));
+                }
+            }
+        }
+        __syncthreads();   // every group's dots are done: the partials may overwrite the inputs
+        if (active) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                float* rr = red + ((grp * GEMV_WAVES + w) * RT + r) * 128;
+                rr[16 * jt + g] = acc[r][0];
+                rr[16 * jt + g + 8] = acc[r][1];
+            }
+        }
+        __syncthreads();
+        if (tid < RT * 128) {
+            const int r = tid >> 7, n = tid & 127;
+#pragma unroll
+            for (int j = 0; j < OWNER_GROUPS; ++j) {
+                if (s0 + uint32_t(j) >= a.splits) break;
+                const float* pj = red + (j * GEMV_WAVES * RT + r) * 128 + n;
+                float v = pj[0];
+#pragma unroll
+                for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + pj[ww * RT * 128];
+                sum = sum + v;
+            }
+        }
+        __syncthreads();   // the partials are read before the next pass's inputs overwrite them
+    }
+    float* rows = reinterpret_cast<float*>(smem);   // [RT][128]
+    if (tid < RT * 128) rows[tid] = sum;
+    __syncthreads();
+    const int wv = tid >> 6;
+    if (wv < RT && uint32_t(wv) < a.rows) {
+        const ColumnOperands op = column_operands(gw, int(c));
+        float z0 = rows[wv * 128 + lane], z1 = rows[wv * 128 + lane + 64];
+        h32_wave(z0, z1);
+        const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
+        float* yr = y + wv * a.y_row_stride;
+        const float o0 = output_value(z0, op.sv0, gw.bias != nullptr, op.b0, a.alpha, a.beta, yr + n0);
+        const float o1 = output_value(z1, op.sv1, gw.bias != nullptr, op.b1, a.alpha, a.beta, yr + n1);
+        *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+        *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+    }
+}
+
 // Second launch of the two-kernel path: fold + output stage per column group.
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a);
 
@@ -509,6 +642,9 @@ struct GemvLaunch {
 
 template <int K>
 hipError_t gemv_dispatch(const GemvLaunch& l);
+// Owner-fold launch: grid = groups * ncg workgroups of OWNER_THREADS.
+template <int K>
+hipError_t gemv_owner_dispatch(const GemvLaunch& l);
 template <int K>
 hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t I, uint32_t N, uint64_t bytes,
                            _Float16* q, hipStream_t stream);
@@ -527,6 +663,21 @@ hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t 
         const int rt = int(l.rows_template);                                                              \
         const int ri = rt <= 4 ? rt - 1 : rt == 6 ? 4 : 5;                                                \
         hipLaunchKernelGGL(table[l.codebook][ri], l.grid, dim3(GEMV_THREADS), l.lds, l.stream, l.args);   \
+        return hipGetLastError();                                                                         \
+    }                                                                                                     \
+    template <>                                                                                           \
+    hipError_t gemv_owner_dispatch<K>(const GemvLaunch& l) {                                              \
+        using Fn = void (*)(GemvArgs);                                                                    \
+        static const Fn table[3][6] = {                                                                   \
+            {gemv_owner_kernel<K, 0, 1>, gemv_owner_kernel<K, 0, 2>, gemv_owner_kernel<K, 0, 3>,          \
+             gemv_owner_kernel<K, 0, 4>, gemv_owner_kernel<K, 0, 6>, gemv_owner_kernel<K, 0, 8>},         \
+            {gemv_owner_kernel<K, 1, 1>, gemv_owner_kernel<K, 1, 2>, gemv_owner_kernel<K, 1, 3>,          \
+             gemv_owner_kernel<K, 1, 4>, gemv_owner_kernel<K, 1, 6>, gemv_owner_kernel<K, 1, 8>},         \
+            {gemv_owner_kernel<K, 2, 1>, gemv_owner_kernel<K, 2, 2>, gemv_owner_kernel<K, 2, 3>,          \
+             gemv_owner_kernel<K, 2, 4>, gemv_owner_kernel<K, 2, 6>, gemv_owner_kernel<K, 2, 8>}};        \
+        const int rt = int(l.rows_template);                                                              \
+        const int ri = rt <= 4 ? rt - 1 : rt == 6 ? 4 : 5;                                                \
+        hipLaunchKernelGGL(table[l.codebook][ri], l.grid, dim3(OWNER_THREADS), l.lds, l.stream, l.args);  \
         return hipGetLastError();                                                                         \
     }                                                                                                     \
     template <>                                                                                           \

@@ -59,6 +59,18 @@ FusedState fused_state_at(void* base, const DeviceWeights& w, uint64_t /*rows*/,
     return st;
 }
 
+// Grouped plans: the owner-fold plan runs one 16-wave workgroup per column
+// group of every group, so it needs at least one per CU (256) to fill the
+// GPU, and then only beats the split plan when each owner's work is short and
+// the rows are many (measured on MI355X, both folds, R1/R4/R8):
+//   16 x 4096 -> 1024 K5 (128 owners): split  20.1 / 26.4 / 38.4 us, owner 36.7 / 47.7 / 62.7
+//   32 x 4096 -> 1024 K5 (256 owners): split  33.9 / 43.9 / 60.5 us, owner 40.5 / 52.7 / 68.6
+//   64 x 2048 ->  512 K4 (256 owners): split  21.2 / 28.0 / 37.1 us, owner 22.2 / 28.0 / 37.0
+//    8 x 2048 -> 4096 K4 (256 owners): split  21.3 / 27.7 / 37.0 us, owner 21.7 / 27.3 / 35.3
+bool grouped_owner_preferred(const DeviceWeights& geometry, uint32_t groups, uint64_t rows) {
+    return uint64_t(groups) * (geometry.output / 128) >= 256 && geometry.input <= 2048 && rows >= 4;
+}
+
 // Rows per GEMM pass: the fragment buffer of one pass stays below 1 GiB so
 // its buffer resource (32-bit range) and the workspace stay bounded.
 uint64_t gemm_pass_rows(const DeviceWeights& w) {

@@ -189,6 +189,8 @@ _PROTOTYPES = {
     "strix_amd_grouped_plan_status": (_S, [vp, u32, C.POINTER(u32)]),
     "strix_amd_stream_read": (_S, [vp, vp, u64, u32, vp, C.POINTER(Stream)]),
     "strix_amd_gemv_noalloc": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream)]),
+    "strix_amd_set_grouped_fold": (_S, [vp, u32]),
+    "strix_amd_grouped_plan_fold": (_S, [vp, C.POINTER(u32)]),
     "strix_tp_dense_plan_create": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), C.POINTER(vp)]),
     "strix_tp_dense_plan_create_tiled": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), u32, C.POINTER(vp)]),
     "strix_tp_dense_plan_create_splitk": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream), u32, u32,
@@ -212,6 +214,7 @@ _PROTOTYPES = {
 GEMV_POLL_DEFAULT = 1 << 22
 GEMV_GAVE_UP = 1
 GEMV_NOALLOC_SCRATCH_BYTES = 4 << 20
+FOLD_AUTO, FOLD_SPLIT, FOLD_OWNER = 0, 1, 2
 
 _lib = None
 

@@ -66,6 +66,10 @@ class Context:
         """Poll rounds of single-launch GEMV finishers on later submissions (0: give up at once)."""
         abi.check(self.lib.strix_amd_set_gemv_poll_limit(self.handle, int(limit)), "strix_amd_set_gemv_poll_limit")
 
+    def set_grouped_fold(self, fold=abi.FOLD_AUTO):
+        """Fold of grouped plans created later: FOLD_AUTO, FOLD_SPLIT or FOLD_OWNER."""
+        abi.check(self.lib.strix_amd_set_grouped_fold(self.handle, int(fold)), "strix_amd_set_grouped_fold")
+
     def close(self):
         if self.handle:
             abi.check(self.lib.strix_context_destroy(self.handle), "strix_context_destroy")
@@ -329,6 +333,12 @@ class GroupedGemvPlan:
 
     def submit(self):
         abi.check(self.lib.strix_grouped_gemv_plan_submit(self.handle), "strix_grouped_gemv_plan_submit")
+
+    def fold(self):
+        """abi.FOLD_SPLIT or abi.FOLD_OWNER."""
+        f = C.c_uint32()
+        abi.check(self.lib.strix_amd_grouped_plan_fold(self.handle, C.byref(f)), "strix_amd_grouped_plan_fold")
+        return f.value
 
     def status(self, clear=False):
         """Sticky status flags (abi.GEMV_GAVE_UP); synchronises the plan's stream."""

@@ -103,6 +103,24 @@ hipError_t launch_gemv_grouped(const DeviceWeights& g, const GroupWeights* table
     return fake::launch_result();
 }
 
+hipError_t launch_gemv_owner(const DeviceWeights& g, const GroupWeights* table, uint32_t groups,
+                             const LinearCall& c, uint64_t x_group_stride, uint64_t y_group_stride, hipStream_t s) {
+    require(groups > 0 && gemv_owner_fits(g, c.rows), "owner fold shape", "launch_gemv_owner");
+    require(fake::in_live_block(table, groups * sizeof(GroupWeights)), "group table outside device memory",
+            "launch_gemv_owner");
+    const uint64_t xb = ((groups - 1) * x_group_stride + (c.rows - 1) * c.x_row_stride + g.input) * 4;
+    const uint64_t yb = ((groups - 1) * y_group_stride + (c.rows - 1) * c.y_row_stride + g.output) * 4;
+    require(fake::in_live_block(c.x, xb), "grouped input outside device memory", "launch_gemv_owner");
+    require(fake::in_live_block(c.y, yb), "grouped output outside device memory", "launch_gemv_owner");
+    record("gemv_owner", c.rows, c.workspace, nullptr, s, c.alpha, c.beta);
+    return fake::launch_result();
+}
+
+bool gemv_owner_fits(const DeviceWeights& w, uint64_t rows) {
+    const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
+    return rows >= 1 && rows <= 8 && sh.splits > 1;
+}
+
 hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& c, hipStream_t s) {
     check_call(w, c, "launch_gemm");
     require(fake::in_live_block(c.workspace, gemm_workspace_bytes(w, c.rows)), "GEMM workspace too small",

@@ -13,8 +13,10 @@ hold over the whole output:
     M = 128, 512: sampled rows against the oracle; a row's bits depend only on
     its row class, so a call on the rows in reverse order returns the same
     rows in reverse order, bit for bit.
-  * C4 grouped o_a plan (16 x 4096 -> 1024, K5) at R1 and R8: every output
-    of four sampled groups against the oracle, all groups finite.
+  * C4 grouped o_a plan (16 x 4096 -> 1024, K5) at R1 and R8, both folds
+    (split and owner): every output of four sampled groups against the
+    oracle, all groups finite; for every row count 1-8 the owner-fold plan,
+    the split plan and per-group 1-row strix_gemv calls agree bit for bit.
   * TP plans at the reference's own shapes (src/tp_split_api.inc:86-100): the
     q_a || kv pair (5120 -> 1280 and 5120 -> 512) and the SwiGLU pair
     (5120 -> 1152) against the oracle.
@@ -28,7 +30,7 @@ from oracle import codec, linear, moe
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-from strix_trellis import runtime  # noqa: E402
+from strix_trellis import abi, runtime  # noqa: E402
 
 DEV = "cuda:0"
 
@@ -109,15 +111,21 @@ def test_c3_gemm(ctx, I, N, M, K):
     w.destroy()
 
 
+@pytest.mark.parametrize("fold", ["split", "owner"])
 @pytest.mark.parametrize("R", [1, 8])
-def test_c4_grouped_oa(ctx, R):
+def test_c4_grouped_oa(ctx, R, fold):
     G, I, N, K = 16, 4096, 1024, 5
-    print(f"C4 grouped {G} x {I}->{N} K={K} R={R}", flush=True)
+    print(f"C4 grouped {G} x {I}->{N} K={K} R={R} fold={fold}", flush=True)
     layers = [synth.layer(I, N, K, 4900 + g) for g in range(G)]
     ws = [runtime.Weights(ctx, *L, "mul1") for L in layers]
     x = synth.activations(R, G * I, 4950 + R)
     y = torch.full((R, G * N), float("nan"), device=DEV)
-    plan = runtime.GroupedGemvPlan(ws, _dev(x), y, R, igs=I, ogs=N, irs=G * I, ors=G * N)
+    ctx.set_grouped_fold(abi.FOLD_OWNER if fold == "owner" else abi.FOLD_SPLIT)
+    try:
+        plan = runtime.GroupedGemvPlan(ws, _dev(x), y, R, igs=I, ogs=N, irs=G * I, ors=G * N)
+    finally:
+        ctx.set_grouped_fold(abi.FOLD_AUTO)
+    assert plan.fold() == (abi.FOLD_OWNER if fold == "owner" else abi.FOLD_SPLIT)
     plan.submit()
     torch.cuda.synchronize()
     got = y.cpu().numpy()
@@ -126,6 +134,40 @@ def test_c4_grouped_oa(ctx, R):
         q = codec.dequantize_rotated(layers[g][0], K, "mul1")
         synth.gate(got[:, g * N:(g + 1) * N], _oracle(x[:, g * I:(g + 1) * I], layers[g], K, q))
     plan.destroy()
+    for w in ws:
+        w.destroy()
+
+
+@pytest.mark.parametrize("G,I,N,K,bias", [(16, 4096, 1024, 5, False), (3, 2048, 384, 4, True),
+                                           (2, 1024, 640, 6, True)])
+def test_grouped_folds_bit_identical(ctx, G, I, N, K, bias):
+    print(f"grouped folds {G} x {I}->{N} K={K} bias={bias} R=1..8", flush=True)
+    ws = [runtime.Weights(ctx, *synth.layer(I, N, K, 5100 + g, bias=bias), "mul1") for g in range(G)]
+    x = synth.activations(8, G * I, 5150)
+    xd = _dev(x)
+    ref = torch.empty((8, G * N), device=DEV)
+    for g in range(G):
+        for r in range(8):
+            y1 = torch.empty((N,), device=DEV)
+            runtime.gemv(ws[g], xd[r, g * I:(g + 1) * I].contiguous(), y1)
+            ref[r, g * N:(g + 1) * N] = y1
+    for R in range(1, 9):
+        outs = {}
+        for fold in (abi.FOLD_SPLIT, abi.FOLD_OWNER):
+            y = torch.full((R, G * N), float("nan"), device=DEV)
+            ctx.set_grouped_fold(fold)
+            try:
+                plan = runtime.GroupedGemvPlan(ws, xd[:R].contiguous(), y, R, igs=I, ogs=N, irs=G * I, ors=G * N)
+            finally:
+                ctx.set_grouped_fold(abi.FOLD_AUTO)
+            assert plan.fold() == fold
+            for _ in range(2):
+                plan.submit()
+            torch.cuda.synchronize()
+            plan.destroy()
+            outs[fold] = y
+        np.testing.assert_array_equal(_bits(outs[abi.FOLD_OWNER]), _bits(outs[abi.FOLD_SPLIT]), err_msg=f"R{R}")
+        np.testing.assert_array_equal(_bits(outs[abi.FOLD_SPLIT]), _bits(ref[:R]), err_msg=f"R{R} vs strix_gemv")
     for w in ws:
         w.destroy()
 
