@@ -20,8 +20,7 @@ using namespace stx_api;
 
 namespace {
 constexpr uint64_t kMaxGroups = STRIX_TP_MAX_BANK_EXPERTS;
-constexpr uint64_t kAlign = STRIX_TRELLIS_WORKSPACE_ALIGNMENT;
-uint64_t align_up(uint64_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+uint64_t align_up(uint64_t v) { return (v + kWorkspaceAlign - 1) & ~(kWorkspaceAlign - 1); }
 
 struct GroupLayout {
     uint64_t table_offset = 0, state_offset = 0, state_bytes = 0, bytes = 0;
@@ -39,13 +38,13 @@ struct Validated {
 bool view_bytes(uint64_t rows, uint64_t row_stride, uint64_t count, uint64_t group_stride, uint64_t width,
                 uint64_t& out) {
     uint64_t a = 0, b = 0;
-    if (!mul_ok(rows - 1, row_stride, a) || !mul_ok(count - 1, group_stride, b)) return false;
+    if (!checked_mul(rows - 1, row_stride, a) || !checked_mul(count - 1, group_stride, b)) return false;
     if (a > UINT64_MAX - b || a + b > UINT64_MAX - width) return false;
-    return mul_ok(a + b + width, 4, out);
+    return checked_mul(a + b + width, 4, out);
 }
 
 strix_status validate(strix_context c, const strix_grouped_gemv_desc* d, Validated& v) {
-    strix_status s = check_header(d);
+    strix_status s = versioned(d);
     if (s != STRIX_SUCCESS) return s;
     if (!d->weights || d->group_count < 1 || d->group_count > kMaxGroups || d->rows < 1 || d->rows > 8 ||
         d->flags != STRIX_GEMV_ROW_INVARIANT_R1 || !d->input || !d->output)
@@ -75,11 +74,11 @@ strix_status validate(strix_context c, const strix_grouped_gemv_desc* d, Validat
     if (!view_bytes(rows, v.xrs, G, v.xgs, I, v.input_bytes) || !view_bytes(rows, v.yrs, G, v.ygs, N, v.output_bytes) ||
         v.input_bytes > d->input_buffer_bytes || v.output_bytes > d->output_buffer_bytes ||
         reinterpret_cast<uintptr_t>(d->input) % 4 || reinterpret_cast<uintptr_t>(d->output) % 4 ||
-        !span_ok(d->input, v.input_bytes) || !span_ok(d->output, v.output_bytes) ||
-        overlaps(d->input, v.input_bytes, d->output, v.output_bytes))
+        !Span(d->input, v.input_bytes).addressable() || !Span(d->output, v.output_bytes).addressable() ||
+        Span(d->input, v.input_bytes).meets(Span(d->output, v.output_bytes)))
         return STRIX_ERROR_INVALID_ARGUMENT;
     for (strix_weights w : v.weights)
-        if (overlaps(d->input, v.input_bytes, w->base, w->bytes) || overlaps(d->output, v.output_bytes, w->base, w->bytes))
+        if (Span(d->input, v.input_bytes).meets(Span(w->base, w->bytes)) || Span(d->output, v.output_bytes).meets(Span(w->base, w->bytes)))
             return STRIX_ERROR_INVALID_ARGUMENT;
     GroupLayout& L = v.layout;
     L.table_offset = 0;
@@ -107,7 +106,7 @@ extern "C" {
 strix_status strix_grouped_gemv_workspace_bytes(strix_context c, const strix_grouped_gemv_desc* d, uint64_t* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = 0;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     Validated v;
     s = validate(c, d, v);
@@ -119,25 +118,25 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
                                             const strix_stream* stream, strix_grouped_gemv_plan* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = nullptr;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    s = stream_ok(c, stream, hs);
+    s = borrowed_stream(c, stream, hs);
     if (s != STRIX_SUCCESS) return s;
     Validated v;
     s = validate(c, d, v);
     if (s != STRIX_SUCCESS) return s;
     if (d->workspace_bytes < v.layout.bytes) return STRIX_ERROR_INSUFFICIENT_BUFFER;
-    if (!d->workspace || !span_ok(d->workspace, d->workspace_bytes) ||
-        reinterpret_cast<uintptr_t>(d->workspace) % kAlign ||
-        overlaps(d->workspace, d->workspace_bytes, d->input, v.input_bytes) ||
-        overlaps(d->workspace, d->workspace_bytes, d->output, v.output_bytes))
+    if (!d->workspace || !Span(d->workspace, d->workspace_bytes).addressable() ||
+        reinterpret_cast<uintptr_t>(d->workspace) % kWorkspaceAlign ||
+        Span(d->workspace, d->workspace_bytes).meets(Span(d->input, v.input_bytes)) ||
+        Span(d->workspace, d->workspace_bytes).meets(Span(d->output, v.output_bytes)))
         return STRIX_ERROR_INVALID_ARGUMENT;
     for (strix_weights w : v.weights)
-        if (overlaps(d->workspace, d->workspace_bytes, w->base, w->bytes)) return STRIX_ERROR_INVALID_ARGUMENT;
-    if ((s = device_range_ok(c, d->input, v.input_bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, d->output, v.output_bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, d->workspace, d->workspace_bytes, kAlign)) != STRIX_SUCCESS) return s;
+        if (Span(d->workspace, d->workspace_bytes).meets(Span(w->base, w->bytes))) return STRIX_ERROR_INVALID_ARGUMENT;
+    if ((s = device_resident(c, Span(d->input, v.input_bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(d->output, v.output_bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(d->workspace, d->workspace_bytes), kWorkspaceAlign)) != STRIX_SUCCESS) return s;
 
     auto* p = new (std::nothrow) strix_grouped_gemv_plan_impl;
     if (!p) return STRIX_ERROR_OUT_OF_MEMORY;
@@ -160,7 +159,7 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
     const hipError_t done = hipStreamSynchronize(hs);
     if (e != hipSuccess || done != hipSuccess) {
         delete p;
-        return from_hip(e != hipSuccess ? e : done);
+        return status_of(e != hipSuccess ? e : done);
     }
     p->owner_ctx = c;
     p->geometry = v.geometry;
@@ -188,24 +187,24 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
 
 strix_status strix_grouped_gemv_plan_submit(strix_grouped_gemv_plan p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
-    const strix_status s = context_ok(p->owner_ctx);
+    const strix_status s = on_context_device(p->owner_ctx);
     if (s != STRIX_SUCCESS) return s;
     stx::LinearCall call = p->call;
     if (p->owner)
-        return from_hip(stx::launch_gemv_owner(p->geometry, p->table, uint32_t(p->retained.size()), call, p->xgs,
+        return status_of(stx::launch_gemv_owner(p->geometry, p->table, uint32_t(p->retained.size()), call, p->xgs,
                                                p->ygs, p->stream));
     call.gemv_poll_limit = p->owner_ctx->gemv_poll_limit;
     const stx::FusedState* st = p->fused.planes ? &p->fused : nullptr;
     if (!st && stx::gemv_shape(p->geometry.input, p->geometry.output, p->geometry.bits).splits > 1)
         return STRIX_ERROR_BACKEND;
-    return from_hip(stx::launch_gemv_grouped(p->geometry, p->table, uint32_t(p->retained.size()), call, p->xgs,
+    return status_of(stx::launch_gemv_grouped(p->geometry, p->table, uint32_t(p->retained.size()), call, p->xgs,
                                              p->ygs, st, p->stream));
 }
 
 strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan p, uint32_t clear, uint32_t* flags) {
     if (flags) *flags = 0;
     if (!p || !flags) return STRIX_ERROR_INVALID_ARGUMENT;
-    const strix_status s = context_ok(p->owner_ctx);
+    const strix_status s = on_context_device(p->owner_ctx);
     if (s != STRIX_SUCCESS) return s;
     return read_fused_status(p->fused, p->stream, flags, clear);
 }
@@ -218,7 +217,7 @@ strix_status strix_amd_grouped_plan_fold(strix_grouped_gemv_plan p, uint32_t* fo
 }
 
 strix_status strix_amd_set_grouped_fold(strix_context c, uint32_t fold) {
-    const strix_status s = context_ok(c);
+    const strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     if (fold > 2) return STRIX_ERROR_INVALID_ARGUMENT;
     c->grouped_fold = fold;

@@ -1,4 +1,14 @@
-// Handle layouts and validation helpers shared by the C ABI translation units.
+// Handle state of the C ABI and the validation vocabulary its translation
+// units (api_*.cpp) share.  Everything here is internal: the ABI is
+// include/strix_trellis.h plus the MI355X extensions in strix_trellis_amd.h.
+//
+// Vocabulary:
+//   Rules      evaluates checks in order; the first failing one decides the
+//              status and the later ones are not evaluated.
+//   Span       a byte range [at, at + size) with checked arithmetic: whether
+//              it is addressable at all, whether two ranges meet, alignment.
+//   versioned  exact struct_size, ABI version 1 and zero reserved words of a
+//              descriptor header (every descriptor of the ABI carries them).
 #pragma once
 #include "strix_trellis.h"
 #include "strix_trellis_amd.h"
@@ -23,8 +33,8 @@ struct strix_weights_impl {
     void* base = nullptr;     // single private allocation: trellis | suh | svh | bias
     uint64_t bytes = 0;
     uint64_t plans = 0;       // live plans retaining these weights
-    // Single-launch state (tagged planes, epochs, status) of plans created on
-    // these weights.  Graphs captured from a plan may replay after the plan is
+    // Single-launch state (planes, epochs, status) of plans created on these
+    // weights.  Graphs captured from a plan may replay after the plan is
     // destroyed, so the arrays live until the weights are destroyed.
     std::vector<void*> counter_arrays;
 };
@@ -41,41 +51,90 @@ struct strix_linear_plan_impl {
 
 namespace stx_api {
 
+constexpr uint64_t kWorkspaceAlign = STRIX_TRELLIS_WORKSPACE_ALIGNMENT;
+
+class Rules {
+public:
+    // Fails with `otherwise` unless `ok`.
+    Rules& need(bool ok, strix_status otherwise) {
+        if (status_ == STRIX_SUCCESS && !ok) status_ = otherwise;
+        return *this;
+    }
+    // Runs `check` (returning a status) only while every earlier rule held.
+    template <class F>
+    Rules& then(F&& check) {
+        if (status_ == STRIX_SUCCESS) status_ = check();
+        return *this;
+    }
+    bool held() const { return status_ == STRIX_SUCCESS; }
+    strix_status status() const { return status_; }
+
+private:
+    strix_status status_ = STRIX_SUCCESS;
+};
+
+struct Span {
+    uintptr_t at = 0;
+    uint64_t size = 0;
+    Span() = default;
+    Span(const void* p, uint64_t bytes) : at(reinterpret_cast<uintptr_t>(p)), size(bytes) {}
+    void* ptr() const { return reinterpret_cast<void*>(at); }
+    // The range neither wraps the address space nor exceeds SIZE_MAX bytes.
+    bool addressable() const { return size <= SIZE_MAX && size <= UINTPTR_MAX - at; }
+    // Both ranges nonempty and sharing at least one byte.
+    bool meets(const Span& o) const { return size && o.size && at < o.at + o.size && o.at < at + size; }
+    bool aligned(uint64_t a) const { return at % a == 0; }
+};
+
+inline bool checked_mul(uint64_t a, uint64_t b, uint64_t& out) { return !__builtin_mul_overflow(a, b, &out); }
+
 template <class E>
-uint32_t enum_raw(const E& value) {
+uint32_t raw_enum(const E& value) {
     static_assert(sizeof(E) == sizeof(uint32_t), "32-bit enum ABI required");
     uint32_t raw = 0;
     std::memcpy(&raw, &value, sizeof(raw));
     return raw;
 }
 
-// Exact struct_size, ABI version 1, zero reserved words.
 template <class T>
-strix_status check_header(const T* d) {
+strix_status versioned(const T* d) {
     if (!d) return STRIX_ERROR_INVALID_ARGUMENT;
     if (d->struct_size != sizeof(T) || d->abi_version != STRIX_TRELLIS_ABI_VERSION) return STRIX_ERROR_ABI_MISMATCH;
-    for (uint64_t v : d->reserved)
-        if (v) return STRIX_ERROR_INVALID_ARGUMENT;
+    for (uint64_t word : d->reserved)
+        if (word) return STRIX_ERROR_INVALID_ARGUMENT;
     return STRIX_SUCCESS;
 }
 
-struct Call {
-    uint64_t rows = 0;
-    uint64_t input_bytes = 0, output_bytes = 0, workspace_bytes = 0;
-};
+// HIP error -> ABI status: OUT_OF_MEMORY when HIP says so, else BACKEND.
+strix_status status_of(hipError_t e);
 
-strix_status from_hip(hipError_t e);
-bool mul_ok(uint64_t a, uint64_t b, uint64_t& out);
-bool span_ok(const void* p, uint64_t bytes);
-bool overlaps(const void* a, uint64_t an, const void* b, uint64_t bn);
-strix_status context_ok(strix_context c);
-strix_status stream_ok(strix_context c, const strix_stream* s, hipStream_t& out);
-strix_status device_range_ok(strix_context c, const void* p, uint64_t bytes, uint64_t align);
-strix_status tensor_ok(const strix_tensor_desc& t, uint64_t width, uint32_t rank, uint64_t rows, uint64_t& bytes);
-strix_status call_ok(strix_context c, const strix_matmul_desc* d, Call& call);
-strix_status storage_ok(strix_context c, const strix_matmul_desc& d, const Call& call, const void* workspace,
-                        uint64_t bytes);
-stx::LinearCall make_call(const strix_matmul_desc& d, uint64_t rows, void* workspace);
+// The calling thread's current device is the context's.
+strix_status on_context_device(strix_context c);
+// A mandatory stream descriptor; a NULL hip_stream is the device's default
+// stream, any other stream must belong to the context's device.
+strix_status borrowed_stream(strix_context c, const strix_stream* s, hipStream_t& out);
+// [span) lies inside one HIP device allocation on the context's device
+// (empty spans pass): INVALID_ARGUMENT when it is not device memory of that
+// device (or misaligned), INSUFFICIENT_BUFFER when the allocation is shorter.
+strix_status device_resident(strix_context c, Span span, uint64_t align);
+
+// One linear call (strix_gemv / strix_gemm / plans): the host-side facts of a
+// descriptor and the device-side checks of its buffers.
+struct LinearExtent {
+    uint64_t rows = 0;
+    Span x, y;                 // logical bytes read and written
+    uint64_t workspace = 0;    // bytes the call needs
+};
+// Rank 1 [width] or rank 2 [rows][width] contiguous F32 tensor.
+strix_status tensor_extent(const strix_tensor_desc& t, uint64_t width, uint32_t rank, uint64_t rows, Span& out);
+// Descriptor, weights, scalars, tensors, required workspace, aliasing of the
+// tensors and the weights (no device memory is inspected).
+strix_status describe_linear(strix_context c, const strix_matmul_desc* d, LinearExtent& e);
+// The workspace (declared range) against the call, then device residence of
+// every buffer.
+strix_status place_linear(strix_context c, const strix_matmul_desc& d, const LinearExtent& e, Span workspace);
+stx::LinearCall to_call(const strix_matmul_desc& d, uint64_t rows, void* workspace);
+
 // Enqueue the initial contents of a single-launch state of `bytes` at base:
 // status and epochs 0, every plane word GEMV_PLANE_EMPTY.
 hipError_t init_fused_state(void* base, uint64_t bytes, uint64_t planes_offset, hipStream_t hs);

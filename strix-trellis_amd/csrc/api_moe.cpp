@@ -32,28 +32,27 @@ struct strix_tp_moe_plan_impl {
 };
 
 namespace {
-constexpr uint64_t kAlign = STRIX_TRELLIS_WORKSPACE_ALIGNMENT;
-uint64_t align_up(uint64_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+uint64_t align_up(uint64_t v) { return (v + kWorkspaceAlign - 1) & ~(kWorkspaceAlign - 1); }
 
 // F32 [rows][width] row view: unit channel stride, row stride >= width.
 strix_status row_view_ok(const strix_tensor_desc& t, uint64_t width, uint64_t rows, uint64_t& stride,
                          uint64_t& bytes) {
-    strix_status s = check_header(&t);
+    strix_status s = versioned(&t);
     if (s != STRIX_SUCCESS) return s;
-    if (enum_raw(t.dtype) != STRIX_DTYPE_F32 || t.rank != 2 || t.shape[0] != rows || t.shape[1] != width ||
+    if (raw_enum(t.dtype) != STRIX_DTYPE_F32 || t.rank != 2 || t.shape[0] != rows || t.shape[1] != width ||
         t.strides[1] != 1 || t.strides[0] < width)
         return STRIX_ERROR_UNSUPPORTED_FORMAT;
     stride = t.strides[0];
     uint64_t span = 0;
-    if (!mul_ok(rows - 1, stride, span) || span > UINT64_MAX - width || !mul_ok(span + width, 4, bytes) ||
-        !span_ok(t.data, bytes))
+    if (!checked_mul(rows - 1, stride, span) || span > UINT64_MAX - width || !checked_mul(span + width, 4, bytes) ||
+        !Span(t.data, bytes).addressable())
         return STRIX_ERROR_INVALID_ARGUMENT;
     if (bytes > t.buffer_bytes) return STRIX_ERROR_INSUFFICIENT_BUFFER;
     if (!t.data || reinterpret_cast<uintptr_t>(t.data) % alignof(float)) return STRIX_ERROR_INVALID_ARGUMENT;
     return STRIX_SUCCESS;
 }
 
-bool touches(const void* p, uint64_t bytes, strix_weights w) { return overlaps(p, bytes, w->base, w->bytes); }
+bool touches(const void* p, uint64_t bytes, strix_weights w) { return Span(p, bytes).meets(Span(w->base, w->bytes)); }
 
 struct MoeValidated {
     std::vector<stx::MoeExpert> bank;
@@ -71,13 +70,13 @@ strix_status common_check(strix_context c, const D* d, uint64_t routes_per_row, 
     if (d->input.rank != 2 || d->input.shape[0] < 1 || d->input.shape[0] > STRIX_TP_MAX_ROWS)
         return STRIX_ERROR_UNSUPPORTED_FORMAT;
     const uint64_t rows = d->input.shape[0];
-    if (!d->experts || d->expert_count < 1 || !span_ok(d->experts, d->expert_count * sizeof(strix_tp_expert_desc)))
+    if (!d->experts || d->expert_count < 1 || !Span(d->experts, d->expert_count * sizeof(strix_tp_expert_desc)).addressable())
         return STRIX_ERROR_INVALID_ARGUMENT;
     if (routes_per_row < 1 || routes_per_row > stx::MOE_MAX_TOPK || rows * routes_per_row > stx::MOE_MAX_ROUTES ||
         d->expert_count < routes_per_row)
         return STRIX_ERROR_INVALID_ARGUMENT;
     // Geometry from the first expert; every weight must match it.
-    strix_status s = check_header(&d->experts[0]);
+    strix_status s = versioned(&d->experts[0]);
     if (s != STRIX_SUCCESS) return s;
     if (!d->experts[0].gate) return STRIX_ERROR_INVALID_ARGUMENT;
     const uint32_t I = d->experts[0].gate->dev.input, H = d->experts[0].gate->dev.output;
@@ -87,11 +86,11 @@ strix_status common_check(strix_context c, const D* d, uint64_t routes_per_row, 
     if (s != STRIX_SUCCESS) return s;
     s = row_view_ok(d->output, I, rows, v.args.y_stride, v.y_bytes);
     if (s != STRIX_SUCCESS) return s;
-    if (overlaps(d->input.data, v.x_bytes, d->output.data, v.y_bytes)) return STRIX_ERROR_INVALID_ARGUMENT;
+    if (Span(d->input.data, v.x_bytes).meets(Span(d->output.data, v.y_bytes))) return STRIX_ERROR_INVALID_ARGUMENT;
     v.bank.resize(d->expert_count);
     for (uint64_t i = 0; i < d->expert_count; ++i) {
         const strix_tp_expert_desc& e = d->experts[i];
-        s = check_header(&e);
+        s = versioned(&e);
         if (s != STRIX_SUCCESS) return s;
         if (e.flags) return STRIX_ERROR_INVALID_ARGUMENT;
         const strix_weights ws[3] = {e.gate, e.up, e.down};
@@ -140,7 +139,7 @@ strix_status common_check(strix_context c, const D* d, uint64_t routes_per_row, 
 
 // Host routes: exact union, ids distinct per row, finite non-negative scores.
 strix_status host_check(strix_context c, const strix_tp_moe_desc* d, MoeValidated& v) {
-    strix_status s = check_header(d);
+    strix_status s = versioned(d);
     if (s != STRIX_SUCCESS) return s;
     if (d->input.rank != 2 || d->input.shape[0] < 1 || d->input.shape[0] > STRIX_TP_MAX_ROWS)
         return STRIX_ERROR_UNSUPPORTED_FORMAT;
@@ -151,8 +150,8 @@ strix_status host_check(strix_context c, const strix_tp_moe_desc* d, MoeValidate
     const uint64_t k = d->route_ids_count / rows;
     s = common_check(c, d, k, v);
     if (s != STRIX_SUCCESS) return s;
-    if (d->expert_count > rows * k || !span_ok(d->route_ids, d->route_ids_count * 4) ||
-        !span_ok(d->route_scores, d->route_scores_count * 4))
+    if (d->expert_count > rows * k || !Span(d->route_ids, d->route_ids_count * 4).addressable() ||
+        !Span(d->route_scores, d->route_scores_count * 4).addressable())
         return STRIX_ERROR_INVALID_ARGUMENT;
     std::unordered_map<uint32_t, uint32_t> index;
     for (uint64_t i = 0; i < d->expert_count; ++i)
@@ -180,7 +179,7 @@ strix_status host_check(strix_context c, const strix_tp_moe_desc* d, MoeValidate
 
 // Device routes: bank ids are positions, routes are device buffers [rows][k].
 strix_status device_check(strix_context c, const strix_tp_moe_device_desc* d, MoeValidated& v) {
-    strix_status s = check_header(d);
+    strix_status s = versioned(d);
     if (s != STRIX_SUCCESS) return s;
     if (d->input.rank != 2 || d->input.shape[0] < 1 || d->input.shape[0] > STRIX_TP_MAX_ROWS)
         return STRIX_ERROR_UNSUPPORTED_FORMAT;
@@ -194,11 +193,11 @@ strix_status device_check(strix_context c, const strix_tp_moe_device_desc* d, Mo
     if (d->expert_count > STRIX_TP_MAX_BANK_EXPERTS) return STRIX_ERROR_INVALID_ARGUMENT;
     for (uint64_t i = 0; i < d->expert_count; ++i)
         if (d->experts[i].expert_id != i) return STRIX_ERROR_INVALID_ARGUMENT;
-    if ((s = device_range_ok(c, d->route_ids, d->route_ids_bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, d->route_scores, d->route_scores_bytes, 4)) != STRIX_SUCCESS) return s;
-    if (overlaps(d->route_ids, d->route_ids_bytes, d->route_scores, d->route_scores_bytes) ||
-        overlaps(d->route_ids, d->route_ids_bytes, d->output.data, v.y_bytes) ||
-        overlaps(d->route_scores, d->route_scores_bytes, d->output.data, v.y_bytes))
+    if ((s = device_resident(c, Span(d->route_ids, d->route_ids_bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(d->route_scores, d->route_scores_bytes), 4)) != STRIX_SUCCESS) return s;
+    if (Span(d->route_ids, d->route_ids_bytes).meets(Span(d->route_scores, d->route_scores_bytes)) ||
+        Span(d->route_ids, d->route_ids_bytes).meets(Span(d->output.data, v.y_bytes)) ||
+        Span(d->route_scores, d->route_scores_bytes).meets(Span(d->output.data, v.y_bytes)))
         return STRIX_ERROR_INVALID_ARGUMENT;
     v.args.ids = d->route_ids;
     v.args.scores = d->route_scores;
@@ -210,16 +209,16 @@ template <class D>
 strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidated& v, strix_tp_moe_plan* out) {
     strix_status s;
     if (d->workspace_bytes < v.hidden_bytes) return STRIX_ERROR_INSUFFICIENT_BUFFER;
-    if (!d->workspace || !span_ok(d->workspace, d->workspace_bytes) ||
-        reinterpret_cast<uintptr_t>(d->workspace) % kAlign ||
-        overlaps(d->workspace, d->workspace_bytes, d->input.data, v.x_bytes) ||
-        overlaps(d->workspace, d->workspace_bytes, d->output.data, v.y_bytes))
+    if (!d->workspace || !Span(d->workspace, d->workspace_bytes).addressable() ||
+        reinterpret_cast<uintptr_t>(d->workspace) % kWorkspaceAlign ||
+        Span(d->workspace, d->workspace_bytes).meets(Span(d->input.data, v.x_bytes)) ||
+        Span(d->workspace, d->workspace_bytes).meets(Span(d->output.data, v.y_bytes)))
         return STRIX_ERROR_INVALID_ARGUMENT;
     for (strix_weights w : v.retained)
         if (touches(d->workspace, d->workspace_bytes, w)) return STRIX_ERROR_INVALID_ARGUMENT;
-    if ((s = device_range_ok(c, d->input.data, v.x_bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, d->output.data, v.y_bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, d->workspace, d->workspace_bytes, kAlign)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(d->input.data, v.x_bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(d->output.data, v.y_bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(d->workspace, d->workspace_bytes), kWorkspaceAlign)) != STRIX_SUCCESS) return s;
 
     stx::MoeArgs& a = v.args;
     const uint32_t routes = a.rows * a.topk;
@@ -233,7 +232,7 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     hipError_t e = hipMalloc(&p->device, table_bytes + route_bytes + counter_bytes + partial_bytes);
     if (e != hipSuccess) {
         delete p;
-        return e == hipErrorOutOfMemory ? STRIX_ERROR_OUT_OF_MEMORY : from_hip(e);
+        return e == hipErrorOutOfMemory ? STRIX_ERROR_OUT_OF_MEMORY : status_of(e);
     }
     char* base = static_cast<char*>(p->device);
     a.bank = reinterpret_cast<const stx::MoeExpert*>(base);
@@ -258,7 +257,7 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     if (e != hipSuccess || done != hipSuccess) {
         (void)hipFree(p->device);
         delete p;
-        return from_hip(e != hipSuccess ? e : done);
+        return status_of(e != hipSuccess ? e : done);
     }
     p->owner = c;
     p->stream = hs;
@@ -271,7 +270,7 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
 
 strix_status plan_ok(strix_tp_moe_plan p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
-    return context_ok(p->owner);
+    return on_context_device(p->owner);
 }
 }  // namespace
 
@@ -302,7 +301,7 @@ void strix_tp_moe_device_desc_init(strix_tp_moe_device_desc* d) {
 strix_status strix_tp_moe_workspace_bytes(strix_context c, const strix_tp_moe_desc* d, uint64_t* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = 0;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     MoeValidated v;
     try {
@@ -318,10 +317,10 @@ strix_status strix_tp_moe_plan_create(strix_context c, const strix_tp_moe_desc* 
                                       strix_tp_moe_plan* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = nullptr;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
     try {
         MoeValidated v;
         if ((s = host_check(c, d, v)) != STRIX_SUCCESS) return s;
@@ -335,10 +334,10 @@ strix_status strix_tp_moe_plan_create_device(strix_context c, const strix_tp_moe
                                              const strix_stream* stream, strix_tp_moe_plan* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = nullptr;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
     try {
         MoeValidated v;
         if ((s = device_check(c, d, v)) != STRIX_SUCCESS) return s;
@@ -382,13 +381,13 @@ strix_status strix_tp_moe_plan_down_reference_core(strix_tp_moe_plan) { return S
 strix_status strix_tp_moe_plan_gate_up(strix_tp_moe_plan p) {
     const strix_status s = plan_ok(p);
     if (s != STRIX_SUCCESS) return s;
-    return from_hip(stx::launch_moe_gate_up(p->args, p->stream));
+    return status_of(stx::launch_moe_gate_up(p->args, p->stream));
 }
 
 strix_status strix_tp_moe_plan_down(strix_tp_moe_plan p) {
     const strix_status s = plan_ok(p);
     if (s != STRIX_SUCCESS) return s;
-    return from_hip(stx::launch_moe_down(p->args, p->stream));
+    return status_of(stx::launch_moe_down(p->args, p->stream));
 }
 
 strix_status strix_tp_moe_plan_submit(strix_tp_moe_plan p) {
@@ -396,29 +395,29 @@ strix_status strix_tp_moe_plan_submit(strix_tp_moe_plan p) {
     if (s != STRIX_SUCCESS) return s;
     hipError_t e = stx::launch_moe_gate_up(p->args, p->stream);
     if (e == hipSuccess) e = stx::launch_moe_down(p->args, p->stream);
-    return from_hip(e);
+    return status_of(e);
 }
 
 strix_status strix_amd_swiglu(strix_context c, const float* gate, const float* up, float* hidden, uint64_t count,
                               const strix_stream* stream) {
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
     if (!count) return STRIX_SUCCESS;
     uint64_t bytes = 0;
-    if (!mul_ok(count, sizeof(float), bytes)) return STRIX_ERROR_INVALID_ARGUMENT;
-    if ((s = device_range_ok(c, gate, bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, up, bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, hidden, bytes, 4)) != STRIX_SUCCESS) return s;
-    return from_hip(stx::launch_moe_swiglu(gate, up, hidden, count, hs));
+    if (!checked_mul(count, sizeof(float), bytes)) return STRIX_ERROR_INVALID_ARGUMENT;
+    if ((s = device_resident(c, Span(gate, bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(up, bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(hidden, bytes), 4)) != STRIX_SUCCESS) return s;
+    return status_of(stx::launch_moe_swiglu(gate, up, hidden, count, hs));
 }
 
 strix_status strix_tp_moe_plan_destroy(strix_tp_moe_plan p) {
     const strix_status s = plan_ok(p);
     if (s != STRIX_SUCCESS) return s;
     const hipError_t e = hipFree(p->device);
-    if (e != hipSuccess) return from_hip(e);
+    if (e != hipSuccess) return status_of(e);
     for (strix_weights w : p->retained) --w->plans;
     delete p;
     return STRIX_SUCCESS;

@@ -13,20 +13,21 @@ static_assert(STRIX_AMD_GEMV_NOALLOC_SCRATCH_BYTES == stx::kGemvScratchBytes, "s
 
 extern "C" strix_status strix_amd_gemv_noalloc(strix_context c, const strix_matmul_desc* d,
                                                const strix_stream* stream) {
-    strix_status s = context_ok(c);
-    if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
-    Call call{};
-    if ((s = call_ok(c, d, call)) != STRIX_SUCCESS) return s;
-    if (d->workspace || d->workspace_bytes) return STRIX_ERROR_INVALID_ARGUMENT;
-    if (call.rows > 8) return STRIX_ERROR_UNSUPPORTED_FORMAT;
-    if (!call.rows) return STRIX_SUCCESS;
+    LinearExtent e;
+    Rules r;
+    r.then([&] { return on_context_device(c); })
+        .then([&] { return borrowed_stream(c, stream, hs); })
+        .then([&] { return describe_linear(c, d, e); });
+    if (!r.held()) return r.status();
+    r.need(!d->workspace && !d->workspace_bytes, STRIX_ERROR_INVALID_ARGUMENT)
+        .need(e.rows <= 8, STRIX_ERROR_UNSUPPORTED_FORMAT);
+    if (!r.held() || !e.rows) return r.status();
     const stx::DeviceWeights& w = d->weights->dev;
-    if (stx::gemv_workspace_bytes(w, uint32_t(call.rows)) > stx::kGemvScratchBytes)
-        return STRIX_ERROR_INSUFFICIENT_BUFFER;
-    if ((s = device_range_ok(c, d->input.data, call.input_bytes, alignof(float))) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, d->output.data, call.output_bytes, alignof(float))) != STRIX_SUCCESS) return s;
-    if (!c->gemv_scratch) return STRIX_ERROR_BACKEND;
-    return from_hip(stx::launch_gemv(w, make_call(*d, call.rows, c->gemv_scratch), hs));
+    r.need(stx::gemv_workspace_bytes(w, uint32_t(e.rows)) <= stx::kGemvScratchBytes, STRIX_ERROR_INSUFFICIENT_BUFFER)
+        .then([&] { return device_resident(c, e.x, alignof(float)); })
+        .then([&] { return device_resident(c, e.y, alignof(float)); })
+        .need(c->gemv_scratch != nullptr, STRIX_ERROR_BACKEND)
+        .then([&] { return status_of(stx::launch_gemv(w, to_call(*d, e.rows, c->gemv_scratch), hs)); });
+    return r.status();
 }

@@ -56,9 +56,9 @@ namespace {
 // F32 rank-1 [width] or rank-2 [rows][width] row view.
 strix_status view_ok(const strix_tensor_desc& t, uint64_t width, uint32_t rank, uint64_t rows, uint64_t& stride,
                      uint64_t& bytes) {
-    strix_status s = check_header(&t);
+    strix_status s = versioned(&t);
     if (s != STRIX_SUCCESS) return s;
-    if (enum_raw(t.dtype) != STRIX_DTYPE_F32 || t.rank != rank) return STRIX_ERROR_UNSUPPORTED_FORMAT;
+    if (raw_enum(t.dtype) != STRIX_DTYPE_F32 || t.rank != rank) return STRIX_ERROR_UNSUPPORTED_FORMAT;
     if (rank == 1) {
         if (t.shape[0] != width || t.shape[1] || t.strides[0] != 1 || t.strides[1]) return STRIX_ERROR_UNSUPPORTED_FORMAT;
         stride = width;
@@ -68,15 +68,15 @@ strix_status view_ok(const strix_tensor_desc& t, uint64_t width, uint32_t rank, 
         stride = t.strides[0];
     }
     uint64_t span = 0;
-    if (!mul_ok(rows - 1, stride, span) || span > UINT64_MAX - width || !mul_ok(span + width, 4, bytes) ||
-        !span_ok(t.data, bytes))
+    if (!checked_mul(rows - 1, stride, span) || span > UINT64_MAX - width || !checked_mul(span + width, 4, bytes) ||
+        !Span(t.data, bytes).addressable())
         return STRIX_ERROR_INVALID_ARGUMENT;
     if (bytes > t.buffer_bytes) return STRIX_ERROR_INSUFFICIENT_BUFFER;
     if (!t.data || reinterpret_cast<uintptr_t>(t.data) % alignof(float)) return STRIX_ERROR_INVALID_ARGUMENT;
     return STRIX_SUCCESS;
 }
 
-bool touches(const void* p, uint64_t bytes, strix_weights w) { return overlaps(p, bytes, w->base, w->bytes); }
+bool touches(const void* p, uint64_t bytes, strix_weights w) { return Span(p, bytes).meets(Span(w->base, w->bytes)); }
 
 // Row count of an input view: rank 1 is R = 1; rank 2 takes shape[0].
 strix_status rows_of(const strix_tensor_desc& in, uint64_t& rows) {
@@ -95,10 +95,10 @@ strix_status member_ok(strix_context c, strix_weights w, const strix_tensor_desc
     if (s != STRIX_SUCCESS) return s;
     s = view_ok(out, w->dev.output, in.rank, rows, ys, y_bytes);
     if (s != STRIX_SUCCESS) return s;
-    if (overlaps(in.data, x_bytes, out.data, y_bytes) || touches(in.data, x_bytes, w) || touches(out.data, y_bytes, w))
+    if (Span(in.data, x_bytes).meets(Span(out.data, y_bytes)) || touches(in.data, x_bytes, w) || touches(out.data, y_bytes, w))
         return STRIX_ERROR_INVALID_ARGUMENT;
-    if ((s = device_range_ok(c, in.data, x_bytes, 4)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, out.data, y_bytes, 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(in.data, x_bytes), 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(out.data, y_bytes), 4)) != STRIX_SUCCESS) return s;
     m.weights = w;
     m.call.x = static_cast<const float*>(in.data);
     m.call.y = static_cast<float*>(out.data);
@@ -145,11 +145,11 @@ strix_status dense_create(strix_context c, const strix_matmul_desc* d, const str
                           uint32_t rows_per_block, bool workspace_allowed, strix_tp_dense_plan* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = nullptr;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
-    if ((s = check_header(d)) != STRIX_SUCCESS) return s;
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
+    if ((s = versioned(d)) != STRIX_SUCCESS) return s;
     if (!workspace_allowed && (d->workspace || d->workspace_bytes)) return STRIX_ERROR_INVALID_ARGUMENT;
     uint64_t rows = 0;
     if ((s = rows_of(d->input, rows)) != STRIX_SUCCESS) return s;
@@ -176,11 +176,11 @@ template <class Out>
 strix_status pair_create(strix_context c, const strix_tp_dense_pair_desc* d, const strix_stream* stream, Out* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = nullptr;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
-    if ((s = check_header(d)) != STRIX_SUCCESS) return s;
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
+    if ((s = versioned(d)) != STRIX_SUCCESS) return s;
     uint64_t rows = 0;
     if ((s = rows_of(d->input, rows)) != STRIX_SUCCESS) return s;
     if (d->rows_per_block > rows || d->strategy > STRIX_TP_SPLITK_TWO) return STRIX_ERROR_INVALID_ARGUMENT;
@@ -192,7 +192,7 @@ strix_status pair_create(strix_context c, const strix_tp_dense_pair_desc* d, con
             STRIX_SUCCESS)
             return s;
     }
-    if (m[0].weights->dev.input != m[1].weights->dev.input || overlaps(m[0].call.y, yb[0], m[1].call.y, yb[1]) ||
+    if (m[0].weights->dev.input != m[1].weights->dev.input || Span(m[0].call.y, yb[0]).meets(Span(m[1].call.y, yb[1])) ||
         touches(m[0].call.y, yb[0], m[1].weights) || touches(m[1].call.y, yb[1], m[0].weights))
         return STRIX_ERROR_INVALID_ARGUMENT;
     auto* p = new (std::nothrow) strix_tp_dense_pair_plan_impl;
@@ -210,17 +210,17 @@ strix_status pair_create(strix_context c, const strix_tp_dense_pair_desc* d, con
 
 strix_status plan_submit(strix_tp_dense_plan_impl* p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
-    const strix_status s = context_ok(p->owner);
+    const strix_status s = on_context_device(p->owner);
     if (s != STRIX_SUCCESS) return s;
     for (const TpMember& m : p->members) {
         const hipError_t e = launch_member(m, p->stream);
-        if (e != hipSuccess) return from_hip(e);
+        if (e != hipSuccess) return status_of(e);
     }
     if (p->swiglu) {
         for (uint64_t r = 0; r < p->rows; ++r) {
             const hipError_t e = stx::launch_moe_swiglu(p->gate + r * p->width, p->up + r * p->width,
                                                         p->hidden + r * p->hidden_stride, p->width, p->stream);
-            if (e != hipSuccess) return from_hip(e);
+            if (e != hipSuccess) return status_of(e);
         }
     }
     return STRIX_SUCCESS;
@@ -228,11 +228,11 @@ strix_status plan_submit(strix_tp_dense_plan_impl* p) {
 
 strix_status plan_destroy(strix_tp_dense_plan_impl* p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
-    const strix_status s = context_ok(p->owner);
+    const strix_status s = on_context_device(p->owner);
     if (s != STRIX_SUCCESS) return s;
     if (p->scratch) {
         const hipError_t e = hipFree(p->scratch);
-        if (e != hipSuccess) return from_hip(e);
+        if (e != hipSuccess) return status_of(e);
     }
     for (TpMember& m : p->members) --m.weights->plans;
     delete p;
@@ -287,9 +287,9 @@ strix_status strix_tp_dense_workspace_bytes(strix_context c, const strix_matmul_
                                             uint64_t* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = 0;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
-    if ((s = check_header(d)) != STRIX_SUCCESS) return s;
+    if ((s = versioned(d)) != STRIX_SUCCESS) return s;
     uint64_t rows = 0;
     if ((s = rows_of(d->input, rows)) != STRIX_SUCCESS) return s;
     return zero_query(rows_per_block > rows ? STRIX_ERROR_INVALID_ARGUMENT : STRIX_SUCCESS, out);
@@ -325,9 +325,9 @@ strix_status strix_tp_dense_plan_destroy(strix_tp_dense_plan p) { return plan_de
 strix_status strix_tp_dense_pair_workspace_bytes(strix_context c, const strix_tp_dense_pair_desc* d, uint64_t* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = 0;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
-    return check_header(d);
+    return versioned(d);
 }
 
 strix_status strix_tp_dense_pair_plan_create(strix_context c, const strix_tp_dense_pair_desc* d,
@@ -359,9 +359,9 @@ strix_status strix_tp_dense_pair_plan_create_r1(strix_context c, const strix_tp_
 strix_status strix_tp_swiglu_workspace_bytes(strix_context c, const strix_tp_swiglu_desc* d, uint64_t* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = 0;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
-    return check_header(d);
+    return versioned(d);
 }
 
 // hidden[r][n] = SwiGLU(gate(x[r])[n], up(x[r])[n]), alpha 1, beta 0 per projection.
@@ -369,11 +369,11 @@ strix_status strix_tp_swiglu_plan_create(strix_context c, const strix_tp_swiglu_
                                          strix_tp_swiglu_plan* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = nullptr;
-    strix_status s = context_ok(c);
+    strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     hipStream_t hs{};
-    if ((s = stream_ok(c, stream, hs)) != STRIX_SUCCESS) return s;
-    if ((s = check_header(d)) != STRIX_SUCCESS) return s;
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
+    if ((s = versioned(d)) != STRIX_SUCCESS) return s;
     uint64_t rows = 0;
     if ((s = rows_of(d->input, rows)) != STRIX_SUCCESS) return s;
     if (d->rows_per_block > rows || d->strategy > STRIX_TP_SPLITK_TWO || !d->gate || !d->up ||
@@ -384,15 +384,15 @@ strix_status strix_tp_swiglu_plan_create(strix_context c, const strix_tp_swiglu_
     const uint64_t H = g.output;
     uint64_t hs_stride = 0, hb = 0;
     if ((s = view_ok(d->hidden_output, H, d->input.rank, rows, hs_stride, hb)) != STRIX_SUCCESS) return s;
-    if ((s = device_range_ok(c, d->hidden_output.data, hb, 4)) != STRIX_SUCCESS) return s;
+    if ((s = device_resident(c, Span(d->hidden_output.data, hb), 4)) != STRIX_SUCCESS) return s;
     const uint64_t diag = rows * H * 4;
     const bool with_diag = d->diagnostic_gate || d->diagnostic_up;
     if (with_diag) {
         if (!d->diagnostic_gate || !d->diagnostic_up || d->diagnostic_bytes < diag ||
-            overlaps(d->diagnostic_gate, diag, d->diagnostic_up, diag))
+            Span(d->diagnostic_gate, diag).meets(Span(d->diagnostic_up, diag)))
             return STRIX_ERROR_INVALID_ARGUMENT;
-        if ((s = device_range_ok(c, d->diagnostic_gate, diag, 4)) != STRIX_SUCCESS) return s;
-        if ((s = device_range_ok(c, d->diagnostic_up, diag, 4)) != STRIX_SUCCESS) return s;
+        if ((s = device_resident(c, Span(d->diagnostic_gate, diag), 4)) != STRIX_SUCCESS) return s;
+        if ((s = device_resident(c, Span(d->diagnostic_up, diag), 4)) != STRIX_SUCCESS) return s;
     }
     auto* p = new (std::nothrow) strix_tp_dense_pair_plan_impl;
     if (!p) return STRIX_ERROR_OUT_OF_MEMORY;
@@ -403,7 +403,7 @@ strix_status strix_tp_swiglu_plan_create(strix_context c, const strix_tp_swiglu_
         const hipError_t e = hipMalloc(&p->scratch, 2 * diag);
         if (e != hipSuccess) {
             delete p;
-            return e == hipErrorOutOfMemory ? STRIX_ERROR_OUT_OF_MEMORY : from_hip(e);
+            return e == hipErrorOutOfMemory ? STRIX_ERROR_OUT_OF_MEMORY : status_of(e);
         }
         p->gate = static_cast<float*>(p->scratch);
         p->up = p->gate + rows * H;
@@ -427,9 +427,9 @@ strix_status strix_tp_swiglu_plan_create(strix_context c, const strix_tp_swiglu_
     uint64_t xb = 0, yb = 0;
     s = member_ok(c, d->gate, d->input, gview, 1.0f, 0.0f, rows, m[0], xb, yb);
     if (s == STRIX_SUCCESS) s = member_ok(c, d->up, d->input, uview, 1.0f, 0.0f, rows, m[1], xb, yb);
-    if (s == STRIX_SUCCESS && (overlaps(d->hidden_output.data, hb, d->input.data, xb) ||
-                               overlaps(d->hidden_output.data, hb, p->gate, diag) ||
-                               overlaps(d->hidden_output.data, hb, p->up, diag)))
+    if (s == STRIX_SUCCESS && (Span(d->hidden_output.data, hb).meets(Span(d->input.data, xb)) ||
+                               Span(d->hidden_output.data, hb).meets(Span(p->gate, diag)) ||
+                               Span(d->hidden_output.data, hb).meets(Span(p->up, diag))))
         s = STRIX_ERROR_INVALID_ARGUMENT;
     if (s == STRIX_SUCCESS) {
         try {

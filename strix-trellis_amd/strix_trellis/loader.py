@@ -1,25 +1,26 @@
 """EXL3 tensor groups from local safetensors files, and their transport to the
 native preparation functions.
 
-Same interface as the reference loader (python/strix_trellis/container.py:
-``SafetensorsFile`` :30-95, ``Exl3Tensor`` :98-240, ``load_exl3`` :243-288;
-docs/LOADER.md), so a caller of the reference can switch to this package:
+The interface is the reference loader's (docs/LOADER.md; names
+``SafetensorsFile``, ``Exl3Tensor``, ``load_exl3``, ``transport_regions`` /
+``transport_buffer`` / ``transport_blob``, ``slice_outputs`` / ``slice_inputs``),
+so loading code moves over unchanged; the product path is the HIP library, so a
+group is ``prepare``d into device weights instead of multiplied on the CPU.
 
-* a ``SafetensorsFile`` parses and validates the header once and maps only the
-  tensors asked for (read-only ``np.memmap``), never a whole shard;
-* ``load_exl3(file, prefix)`` selects one modern EXL3 group -- trellis I16
-  ``[I/16, N/16, 16 K]``, folded F16 ``suh[I]`` / ``svh[N]``, an optional mul1 or
-  mcg marker, an optional F16/F32 bias -- and rejects what the transport
-  contract cannot carry (external out_scales, simultaneous or unknown
-  markers, non-finite scales, overlapping payloads), raising ``ValueError``;
-* an ``Exl3Tensor`` exports the canonical transport -- four little-endian
-  payloads at 4-byte aligned offsets plus the ``strix_exl3_metadata_v1``
-  fields -- as borrowed regions, as one caller-owned buffer, or as an immutable
-  blob, and slices H128-aligned output or input partitions without expanding Q.
+How it is organised here:
 
-One difference: the reference's ``Exl3Tensor.matmul`` is its CPU reference.
-Here the product path is the HIP library, so a group is instead ``prepare``d
-into device weights (``runtime.Weights``) and multiplied there.
+* ``_Catalog`` reads a file's header once (length prefix, JSON object with no
+  duplicate keys) and resolves single tensors to read-only memory maps after
+  checking their dtype, shape, byte range and size -- only the tensors asked
+  for, never a whole shard;
+* ``load_exl3`` picks one modern EXL3 group by the checks in ``_GROUP_CHECKS``
+  order: member tensors, trellis geometry and rate, folded F16 scales, the
+  codebook marker, the optional bias, disjoint payloads.  Anything the
+  transport contract cannot carry is a ``ValueError``;
+* ``_Transport`` lays a group out as the canonical transport (trellis I16,
+  suh/svh F16, bias F32 at 4-byte aligned offsets, plus the
+  ``strix_exl3_metadata_v1`` fields) without copying; the three exports read it;
+* partitions cut H128-aligned column or channel ranges as views of the tiles.
 """
 from dataclasses import dataclass
 import json
@@ -29,109 +30,195 @@ import struct
 
 import numpy as np
 
-# safetensors dtype tags this loader maps; BF16 has no NumPy type and is only
-# mapped as its raw little-endian 16-bit patterns on request.
-_DTYPES = {"I16": np.dtype("<i2"), "I32": np.dtype("<i4"), "F16": np.dtype("<f2"), "F32": np.dtype("<f4")}
-_RAW_BF16 = np.dtype("<u2")
-_MAX_HEADER = 8_000_000
-
-# Codebooks: enum order of strix_exl3_codebook and the multiplier each numeric
-# marker must carry (3inst has no marker).
-CODEBOOKS = ("3inst", "mcg", "mul1")
-MARKERS = {"3inst": 0, "mcg": 0xCBAC1FED, "mul1": 0x83DCD12D}
+CODEBOOKS = ("3inst", "mcg", "mul1")                          # strix_exl3_codebook order
+MARKERS = {"3inst": 0, "mcg": 0xCBAC1FED, "mul1": 0x83DCD12D}  # multiplier a numeric marker carries
 TRANSPORT_VERSION = 1
-# Transport payloads in blob order with their wire dtypes.
-_PAYLOADS = (("trellis", np.dtype("<i2")), ("suh", np.dtype("<f2")), ("svh", np.dtype("<f2")),
-             ("bias", np.dtype("<f4")))
-# Rates the EXL3 format defines: whole bits 1..8, and 1.5 / 2.5 / 3.5 for mul1
-# (CPU only; GPU transport v1 carries whole rates).
-_RATES = {float(k) for k in range(1, 9)} | {1.5, 2.5, 3.5}
+
+_MAP_DTYPES = {"I16": "<i2", "I32": "<i4", "F16": "<f2", "F32": "<f4"}
+_HEADER_LIMIT = 8_000_000
+# Whole rates 1..8 bits, and the half rates the format defines for mul1 (the
+# CPU reference reads them; GPU transport v1 carries whole rates only).
+_WHOLE_RATES = frozenset(float(b) for b in range(1, 9))
+_HALF_RATES = frozenset((1.5, 2.5, 3.5))
 
 
-def _object_without_duplicates(pairs):
-    out = {}
+def _no_duplicate_keys(pairs):
+    seen = {}
     for key, value in pairs:
-        if key in out:
-            raise ValueError(f"Duplicate JSON key: {key}")
-        out[key] = value
-    return out
+        if key in seen:
+            raise ValueError(f"Duplicate JSON key in safetensors header: {key}")
+        seen[key] = value
+    return seen
 
 
-def _int_list(value, length=None):
-    return (isinstance(value, list) and (length is None or len(value) == length) and
-            all(type(v) is int for v in value))
+def _ints(value, count=None):
+    return isinstance(value, list) and all(type(v) is int for v in value) and (count is None or len(value) == count)
 
 
-class SafetensorsFile:
-    """Header of a local safetensors file; tensors are mapped on request.
+@dataclass(frozen=True)
+class _Entry:
+    name: str
+    dtype: np.dtype
+    shape: tuple
+    begin: int
+    end: int
 
-    Only the tensors asked for are validated (range, dtype, element count);
-    unrelated tensors of a multi-format shard need not be understood.  Keep
-    the file unchanged while mapped arrays are alive.
-    """
+
+class _Catalog:
+    """The parsed header of one safetensors file."""
 
     def __init__(self, path):
         self.path = Path(path)
         self.file_bytes = self.path.stat().st_size
         with self.path.open("rb") as f:
-            head = f.read(8)
-            if len(head) != 8:
-                raise ValueError("Truncated safetensors header length")
-            (n,) = struct.unpack("<Q", head)
-            if n < 2 or n > min(_MAX_HEADER, self.file_bytes - 8):
-                raise ValueError("Invalid or oversized safetensors header")
-            text = f.read(n)
+            prefix = f.read(8)
+            if len(prefix) < 8:
+                raise ValueError("Truncated safetensors file: no header length")
+            (length,) = struct.unpack("<Q", prefix)
+            if not 2 <= length <= min(_HEADER_LIMIT, self.file_bytes - 8):
+                raise ValueError("Safetensors header length is invalid or oversized")
+            text = f.read(length)
         try:
-            header = json.loads(text, object_pairs_hook=_object_without_duplicates)
-        except json.JSONDecodeError as e:
-            raise ValueError(f"Invalid safetensors header JSON: {e}") from None
+            header = json.loads(text, object_pairs_hook=_no_duplicate_keys)
+        except json.JSONDecodeError as error:
+            raise ValueError(f"Safetensors header is not valid JSON: {error}") from None
         if not isinstance(header, dict):
-            raise ValueError("Safetensors header must be an object")
+            raise ValueError("Safetensors header is not a JSON object")
         self.header = header
-        self.data_offset = 8 + n
+        self.data_offset = 8 + length
 
-    def tensor(self, name, *, raw_bf16=False):
-        """Read-only map of one tensor (BF16 only with raw_bf16: uint16 bit patterns)."""
+    def entry(self, name, raw_bf16=False):
         info = self.header.get(name)
         tag = info.get("dtype") if isinstance(info, dict) else None
-        if tag in _DTYPES:
-            dtype = _DTYPES[tag]
+        if tag in _MAP_DTYPES:
+            dtype = np.dtype(_MAP_DTYPES[tag])
         elif tag == "BF16" and raw_bf16:
-            dtype = _RAW_BF16
+            dtype = np.dtype("<u2")   # raw bit patterns: BF16 has no NumPy type
         else:
-            raise ValueError(f"Missing tensor or unsupported dtype: {name}")
+            raise ValueError(f"Tensor {name} is missing or has an unsupported dtype")
         shape, offsets = info.get("shape"), info.get("data_offsets")
-        if not _int_list(shape) or len(shape) > 8 or any(v < 0 for v in shape) or not _int_list(offsets, 2):
-            raise ValueError(f"Invalid tensor shape or offsets: {name}")
+        if not (_ints(shape) and len(shape) <= 8 and min(shape, default=0) >= 0 and _ints(offsets, 2)):
+            raise ValueError(f"Tensor {name} has an invalid shape or data_offsets")
         begin, end = offsets
         if not 0 <= begin <= end <= self.file_bytes - self.data_offset:
-            raise ValueError(f"Tensor range exceeds file: {name}")
+            raise ValueError(f"Tensor {name} lies outside the file")
         if math.prod(shape) * dtype.itemsize != end - begin:
-            raise ValueError(f"Tensor size does not match shape/dtype: {name}")
-        if begin == end:
-            empty = np.empty(shape, dtype=dtype)
-            empty.flags.writeable = False
-            return empty
-        return np.memmap(self.path, mode="r", dtype=dtype, offset=self.data_offset + begin, shape=tuple(shape))
+            raise ValueError(f"Tensor {name} byte size does not match its shape and dtype")
+        return _Entry(name, dtype, tuple(shape), begin, end)
+
+    def map(self, e):
+        if e.begin == e.end:
+            out = np.empty(e.shape, dtype=e.dtype)
+            out.flags.writeable = False
+            return out
+        return np.memmap(self.path, mode="r", dtype=e.dtype, offset=self.data_offset + e.begin, shape=e.shape)
+
+
+class SafetensorsFile:
+    """A local safetensors file: its header parsed and validated once; tensors
+    mapped read-only on request.  Only tensors asked for are checked, so a
+    shard may hold others this loader does not understand.  Keep the file
+    unchanged while mapped arrays are alive."""
+
+    def __init__(self, path):
+        self._catalog = _Catalog(path)
+        self.path = self._catalog.path
+        self.header = self._catalog.header
+        self.data_offset = self._catalog.data_offset
+        self.file_bytes = self._catalog.file_bytes
+
+    def tensor(self, name, *, raw_bf16=False):
+        """Read-only map of one tensor (BF16 only with raw_bf16, as uint16 bit patterns)."""
+        return self._catalog.map(self._catalog.entry(name, raw_bf16))
 
     def tensor_float32(self, name):
-        """An unquantized BF16 / F16 / F32 tensor widened (exactly) to a float32 copy."""
-        info = self.header.get(name)
-        tag = info.get("dtype") if isinstance(info, dict) else None
+        """A BF16 / F16 / F32 tensor widened (exactly) into a float32 copy."""
+        e = self._catalog.entry(name, raw_bf16=True)
+        tag = self.header[name]["dtype"]
         if tag not in ("BF16", "F16", "F32"):
-            raise ValueError(f"Not a floating tensor: {name}")
-        raw = self.tensor(name, raw_bf16=True)
+            raise ValueError(f"Tensor {name} is not a floating tensor")
+        raw = self._catalog.map(e)
         if tag == "BF16":
             return (raw.astype(np.uint32) << 16).view(np.float32)
-        return np.asarray(raw, dtype=np.float32).copy()
+        return np.array(raw, dtype=np.float32)
 
     def exl3(self, prefix):
         return load_exl3(self, prefix)
 
 
+# ----------------------------------------------------------------------------
+# Transport layout
+# ----------------------------------------------------------------------------
+@dataclass(frozen=True)
+class _Part:
+    name: str
+    values: np.ndarray
+    dtype: np.dtype
+    offset: int
+    nbytes: int
+
+
+class _Transport:
+    """The canonical transport of a group: payloads in blob order at 4-byte
+    aligned offsets and the strix_exl3_metadata_v1 fields; nothing is copied."""
+
+    WIRE = (("trellis", np.dtype("<i2")), ("suh", np.dtype("<f2")), ("svh", np.dtype("<f2")),
+            ("bias", np.dtype("<f4")))
+
+    def __init__(self, t):
+        if not float(t.bits).is_integer():
+            raise ValueError("GPU transport v1 supports integer bitrates only")
+        self.fields = {"transport_version": TRANSPORT_VERSION, "rows": t.output_size, "columns": t.input_size,
+                       "bits_x2": 2 * int(t.bits), "codebook": CODEBOOKS.index(t.codebook),
+                       "marker": MARKERS[t.codebook]}
+        self.parts, end = [], 0
+        for name, dtype in self.WIRE:
+            values = getattr(t, name)
+            if values is None:
+                self.fields[f"{name}_offset"] = self.fields[f"{name}_bytes"] = 0
+                continue
+            values = np.asarray(values)
+            offset = -(-end // 4) * 4
+            part = _Part(name, values, dtype, offset, values.size * dtype.itemsize)
+            self.fields[f"{name}_offset"], self.fields[f"{name}_bytes"] = part.offset, part.nbytes
+            self.parts.append(part)
+            end = part.offset + part.nbytes
+        self.size = end
+
+    def regions(self):
+        views = {name: None for name, _ in self.WIRE}
+        for p in self.parts:
+            views[p.name] = memoryview(np.ascontiguousarray(p.values, dtype=p.dtype)).cast("B").toreadonly()
+        return views
+
+    def write(self, destination):
+        """Pack into `destination` (a byte view of at least self.size)."""
+        cursor = 0
+        for p in self.parts:
+            destination[cursor:p.offset] = bytes(p.offset - cursor)   # zero the alignment gap
+            typed = np.ndarray(p.values.shape, dtype=p.dtype, buffer=destination, offset=p.offset)
+            np.copyto(typed, p.values, casting="unsafe")
+            cursor = p.offset + p.nbytes
+
+
+def _writable_bytes(buffer):
+    try:
+        view = memoryview(buffer)
+    except TypeError:
+        raise ValueError("Destination must expose a writable, contiguous buffer") from None
+    if view.readonly or not view.c_contiguous:
+        raise ValueError("Destination must be writable and C-contiguous")
+    return view.cast("B")
+
+
+def _checked_cut(begin, end, limit, what):
+    if type(begin) is not int or type(end) is not int or not 0 <= begin < end <= limit or begin % 128 or end % 128:
+        raise ValueError(f"{what} partitions must be nonempty, in range and H128 aligned")
+
+
 @dataclass(frozen=True)
 class Exl3Tensor:
-    """One folded-scale EXL3 linear: logical Q is [input, output]."""
+    """One folded-scale EXL3 linear; the logical Q is [input, output]."""
     trellis: np.ndarray      # int16 [I/16, N/16, 16 * bits]
     suh: np.ndarray          # float16 [I]
     svh: np.ndarray          # float16 [N]
@@ -151,164 +238,155 @@ class Exl3Tensor:
 
     # ---------------------------------------------------------------- partitions
     def slice_outputs(self, begin, end):
-        """H128-aligned output partition [begin, end): a view of its tile columns.
-
-        The output transform is block-diagonal over 128 columns, so each part
-        keeps complete H128 blocks; its trellis is repacked at export only.
-        """
-        if type(begin) is not int or type(end) is not int or not 0 <= begin < end <= self.output_size \
-                or begin % 128 or end % 128:
-            raise ValueError("Output partitions must be nonempty, in range and H128 aligned")
-        return Exl3Tensor(self.trellis[:, begin // 16:end // 16, :], self.suh, self.svh[begin:end], self.bits,
-                          self.codebook, None if self.bias is None else self.bias[begin:end], self.source,
-                          f"{self.prefix}[{begin}:{end}]")
+        """Output columns [begin, end), H128 aligned: the output transform is
+        block diagonal over 128 columns, so each part keeps whole blocks.  The
+        tile columns are a view; the trellis is packed only at export."""
+        _checked_cut(begin, end, self.output_size, "Output")
+        cols = slice(begin // 16, end // 16)
+        bias = None if self.bias is None else self.bias[begin:end]
+        return Exl3Tensor(self.trellis[:, cols, :], self.suh, self.svh[begin:end], self.bits, self.codebook, bias,
+                          self.source, f"{self.prefix}[{begin}:{end}]")
 
     def slice_inputs(self, begin, end, *, include_bias):
-        """H128-aligned input partition [begin, end) for a K-split sum over parts.
-
-        Exactly one part of a sum may carry the bias, so the choice is an
-        explicit bool.  svh stays whole (every part produces all outputs).
-        """
-        if type(begin) is not int or type(end) is not int or not 0 <= begin < end <= self.input_size \
-                or begin % 128 or end % 128:
-            raise ValueError("Input partitions must be nonempty, in range and H128 aligned")
+        """Input channels [begin, end), H128 aligned, for a sum over parts:
+        exactly one part of the sum carries the bias (an explicit bool); svh
+        stays whole, every part producing all outputs."""
+        _checked_cut(begin, end, self.input_size, "Input")
         if type(include_bias) is not bool:
             raise ValueError("include_bias must be an explicit bool")
-        return Exl3Tensor(self.trellis[begin // 16:end // 16], self.suh[begin:end], self.svh, self.bits,
-                          self.codebook, self.bias if include_bias else None, self.source,
-                          f"{self.prefix}[K{begin}:{end}]")
+        rows = slice(begin // 16, end // 16)
+        return Exl3Tensor(self.trellis[rows], self.suh[begin:end], self.svh, self.bits, self.codebook,
+                          self.bias if include_bias else None, self.source, f"{self.prefix}[K{begin}:{end}]")
 
     # ----------------------------------------------------------------- transport
-    def _layout(self):
-        """Payloads, strix_exl3_metadata_v1 fields and blob size; copies nothing."""
-        if not float(self.bits).is_integer():
-            raise ValueError("GPU transport v1 supports integer bitrates only")
-        meta = {"rows": self.output_size, "columns": self.input_size, "bits_x2": int(self.bits) * 2,
-                "codebook": CODEBOOKS.index(self.codebook), "marker": MARKERS[self.codebook],
-                "transport_version": TRANSPORT_VERSION}
-        payloads, pos = [], 0
-        for name, dtype in _PAYLOADS:
-            values = getattr(self, name)
-            if values is None:
-                meta[name + "_offset"] = meta[name + "_bytes"] = 0
-                continue
-            values = np.asarray(values)
-            pos = (pos + 3) & ~3
-            meta[name + "_offset"], meta[name + "_bytes"] = pos, values.size * dtype.itemsize
-            pos += values.size * dtype.itemsize
-            payloads.append((name, values, dtype))
-        return payloads, meta, pos
-
     def transport_regions(self):
-        """(name -> read-only byte view or None, metadata fields).
+        """(name -> read-only byte view, or None for an absent bias; metadata fields).
 
-        A payload that is already contiguous little-endian is borrowed (a
-        mapped file stays mapped); only others (e.g. the strided trellis of an
-        output slice) are packed.  Offsets in the fields describe the
-        equivalent blob; each view starts at its own payload.  The sources
-        must stay unchanged until native preparation returns.
-        """
-        payloads, meta, _ = self._layout()
-        regions = {name: None for name, _ in _PAYLOADS}
-        for name, values, dtype in payloads:
-            regions[name] = memoryview(np.ascontiguousarray(values, dtype=dtype)).cast("B").toreadonly()
-        return regions, meta
+        Contiguous little-endian payloads are borrowed (a mapped file stays
+        mapped); only the others are packed.  The offsets in the fields are
+        those of the equivalent blob; each view starts at its own payload.
+        Keep the sources unchanged until native preparation returns."""
+        layout = _Transport(self)
+        return layout.regions(), layout.fields
 
     def transport_buffer(self, destination=None):
-        """(buffer, metadata fields): the blob written into one buffer.
+        """(buffer, metadata fields): the blob packed into one buffer.
 
-        With no destination a bytearray of the exact size is returned; a
-        given writable C-contiguous buffer (at least that large, not sharing
-        memory with any source) receives the blob in its prefix and a
-        memoryview of that prefix is returned, the rest left untouched.
-        Alignment gaps are zeroed; each payload is copied once, straight into
-        its typed place.
-        """
-        payloads, meta, size = self._layout()
-        owned = destination is None
-        buf = bytearray(size) if owned else destination
-        try:
-            view = memoryview(buf)
-        except TypeError:
-            raise ValueError("Destination must expose a writable contiguous buffer") from None
-        if view.readonly or not view.c_contiguous:
-            raise ValueError("Destination must be writable and C-contiguous")
-        view = view.cast("B")
-        if view.nbytes < size:
+        Without a destination, an exact-size bytearray.  A given writable,
+        C-contiguous destination at least that large and sharing no memory with
+        the sources receives the blob in its prefix (alignment gaps zeroed, the
+        rest untouched); a memoryview of that prefix is returned."""
+        layout = _Transport(self)
+        if destination is None:
+            out = bytearray(layout.size)
+            layout.write(memoryview(out))
+            return out, layout.fields
+        view = _writable_bytes(destination)
+        if view.nbytes < layout.size:
             raise ValueError("Destination is too small for the transport")
-        if not owned:
-            target = np.frombuffer(view, dtype=np.uint8)
-            if any(np.may_share_memory(target, values) for _, values, _ in payloads):
-                raise ValueError("Destination must not overlap transport source arrays")
-        pos = 0
-        for name, values, dtype in payloads:
-            offset = meta[name + "_offset"]
-            view[pos:offset] = bytes(offset - pos)
-            np.copyto(np.ndarray(values.shape, dtype=dtype, buffer=view, offset=offset), values, casting="unsafe")
-            pos = offset + meta[name + "_bytes"]
-        return (buf if owned else view[:size]), meta
+        target = np.frombuffer(view, dtype=np.uint8)
+        if any(np.may_share_memory(target, p.values) for p in layout.parts):
+            raise ValueError("Destination must not overlap the transport's source arrays")
+        layout.write(view)
+        return view[:layout.size], layout.fields
 
     def transport_blob(self):
         """(immutable bytes, metadata fields) for strix_weights_prepare."""
-        buf, meta = self.transport_buffer()
-        return bytes(buf), meta
+        packed, fields = self.transport_buffer()
+        return bytes(packed), fields
 
     # ------------------------------------------------------------------ device
     def prepare(self, ctx, stream=None, *, blob=False):
         """Device weights (``runtime.Weights``) from the transport regions
-        (strix_weights_prepare_parts) or, with blob=True, from the blob
-        (strix_weights_prepare).  The library copies the payloads; the views
-        and mapped file may be released once this returns."""
+        (strix_weights_prepare_parts) or, with blob=True, the blob
+        (strix_weights_prepare).  The library copies the payloads, so the views
+        and the mapped file may be released once this returns."""
         from . import runtime
         return runtime.Weights.from_transport(ctx, self, stream=stream, blob=blob)
 
 
+# ----------------------------------------------------------------------------
+# Group selection
+# ----------------------------------------------------------------------------
+class _Group:
+    """The tensors of one group as they are picked, with their byte ranges."""
+
+    def __init__(self, catalog, prefix):
+        self.catalog, self.prefix, self.picked = catalog, prefix, []
+
+    def has(self, suffix):
+        return self.prefix + suffix in self.catalog.header
+
+    def take(self, suffix):
+        e = self.catalog.entry(self.prefix + suffix)
+        self.picked.append(e)
+        return self.catalog.map(e)
+
+
+def _geometry(trellis):
+    if trellis.dtype != np.dtype("<i2") or trellis.ndim != 3 or 0 in trellis.shape:
+        raise ValueError("EXL3 trellis must be a nonempty I16 array [I/16, O/16, words]")
+    bits = trellis.shape[2] / 16
+    if bits not in _WHOLE_RATES | _HALF_RATES:
+        raise ValueError(f"Unsupported EXL3 bitrate: {bits}")
+    inputs, outputs = 16 * trellis.shape[0], 16 * trellis.shape[1]
+    if inputs % 128 or outputs % 128:
+        raise ValueError("A complete EXL3 linear needs input and output sizes that are multiples of 128")
+    return inputs, outputs, bits
+
+
+def _folded_scale(values, size, name):
+    if values.dtype != np.dtype("<f2") or values.shape != (size,) or not np.isfinite(values).all():
+        raise ValueError(f"Invalid folded F16 scale vector {name}")
+
+
+def _codebook(group):
+    named = [cb for cb in ("mul1", "mcg") if group.has("." + cb)]
+    if len(named) > 1:
+        raise ValueError("Simultaneous mul1 and mcg markers")
+    if not named:
+        return "3inst"
+    marker = group.take("." + named[0])
+    # Empty: the historical marker; numeric: one I32 that carries the multiplier.
+    numeric_ok = marker.dtype == np.dtype("<i4") and marker.size == 1 and \
+        int(marker.reshape(-1)[0]) & 0xFFFFFFFF == MARKERS[named[0]]
+    if marker.size and not numeric_ok:
+        raise ValueError("Unsupported EXL3 codebook marker")
+    return named[0]
+
+
+def _bias(group, outputs):
+    if not group.has(".bias"):
+        return None
+    raw = group.take(".bias")
+    if raw.dtype.kind != "f" or raw.shape != (outputs,) or not np.isfinite(raw).all():
+        raise ValueError("Invalid bias vector")
+    bias = raw.astype(np.float32, copy=False)   # F32 stays mapped, F16 widens once
+    bias.flags.writeable = False
+    return bias
+
+
+def _disjoint(group):
+    ranges = sorted((e.begin, e.end) for e in group.picked if e.end > e.begin)
+    if any(prev[1] > cur[0] for prev, cur in zip(ranges, ranges[1:])):
+        raise ValueError("Selected EXL3 tensors overlap in the file")
+
+
 def load_exl3(file, prefix):
-    """Map and validate the EXL3 group `prefix` of a path or SafetensorsFile."""
-    f = file if isinstance(file, SafetensorsFile) else SafetensorsFile(file)
+    """Map and validate the EXL3 group ``prefix`` of a path or SafetensorsFile."""
+    sf = file if isinstance(file, SafetensorsFile) else SafetensorsFile(file)
     if not isinstance(prefix, str) or not prefix:
         raise ValueError("A nonempty tensor prefix is required")
-    if prefix + ".out_scales" in f.header:
-        raise ValueError("External out_scales requires an explicit scale contract")
-    selected = {}
-
-    def take(suffix):
-        name = prefix + suffix
-        selected[name] = f.tensor(name)
-        return selected[name]
-
-    trellis, suh, svh = take(".trellis"), take(".suh"), take(".svh")
-    if trellis.dtype != np.dtype("<i2") or trellis.ndim != 3 or 0 in trellis.shape:
-        raise ValueError("EXL3 trellis must be nonempty I16 [I/16,O/16,words]")
-    bits = trellis.shape[2] / 16
-    if bits not in _RATES:
-        raise ValueError(f"Unsupported EXL3 bitrate: {bits}")
-    inputs, outputs = trellis.shape[0] * 16, trellis.shape[1] * 16
-    if inputs % 128 or outputs % 128:
-        raise ValueError("Complete EXL3 linear requires I/O multiples of 128")
-    for name, values, size in (("suh", suh, inputs), ("svh", svh, outputs)):
-        if values.dtype != np.dtype("<f2") or values.shape != (size,) or not np.isfinite(values).all():
-            raise ValueError(f"Invalid folded F16 scale vector: {name}")
-    present = [cb for cb in ("mul1", "mcg") if f"{prefix}.{cb}" in f.header]
-    if len(present) > 1:
-        raise ValueError("Simultaneous mul1/mcg markers")
-    codebook = present[0] if present else "3inst"
-    if present:
-        marker = take("." + codebook)
-        # An empty marker is the historical form; a numeric one must carry the multiplier.
-        if marker.size and (marker.dtype != np.dtype("<i4") or marker.size != 1 or
-                            int(marker.reshape(-1)[0]) & 0xFFFFFFFF != MARKERS[codebook]):
-            raise ValueError("Unsupported EXL3 codebook marker")
-    if not bits.is_integer() and codebook != "mul1":
-        raise ValueError("Half-integer EXL3 rates require mul1")
-    bias = None
-    if prefix + ".bias" in f.header:
-        raw = take(".bias")
-        if raw.dtype.kind != "f" or raw.shape != (outputs,) or not np.isfinite(raw).all():
-            raise ValueError("Invalid bias vector")
-        bias = raw.astype(np.float32, copy=False)   # F32 stays mapped, F16 widens once
-        bias.flags.writeable = False
-    spans = sorted(tuple(f.header[name]["data_offsets"]) for name, arr in selected.items() if arr.nbytes)
-    if any(a[1] > b[0] for a, b in zip(spans, spans[1:])):
-        raise ValueError("Overlapping selected EXL3 tensor ranges")
-    return Exl3Tensor(trellis, suh, svh, bits, codebook, bias, str(f.path), prefix)
+    group = _Group(sf._catalog, prefix)
+    if group.has(".out_scales"):
+        raise ValueError("External out_scales need an explicit scale contract; not supported")
+    trellis, suh, svh = group.take(".trellis"), group.take(".suh"), group.take(".svh")
+    inputs, outputs, bits = _geometry(trellis)
+    _folded_scale(suh, inputs, "suh")
+    _folded_scale(svh, outputs, "svh")
+    codebook = _codebook(group)
+    if bits in _HALF_RATES and codebook != "mul1":
+        raise ValueError("Half-integer EXL3 rates require the mul1 codebook")
+    bias = _bias(group, outputs)
+    _disjoint(group)
+    return Exl3Tensor(trellis, suh, svh, bits, codebook, bias, str(sf.path), prefix)

@@ -1,76 +1,84 @@
 """Two-rank tensor-parallel views of EXL3 groups, made at load time.
 
-Same entry point as the reference (python/strix_trellis/tp.py:55-83,
-``rank_partition``; docs/LOADER.md "Views by TP rank"): for the sites of the
-mix-B / expert-TP layout (the site table below, reference tp.py:13-25) rank 0
-or 1 gets
+The entry point is the reference's ``rank_partition(tensor, site, rank,
+bias_rank=0)`` (docs/LOADER.md, "Views by TP rank"); the site table holds the
+shapes and rates of the mix-B / expert-TP layout it partitions.  Per site a
+rank gets
 
-* an H128-aligned half of the output columns (``q_b``, ``*_gate``, ``*_up``);
-  the ranks' outputs are concatenated in rank order;
-* an H128-aligned half of the input channels (``o_b``, ``*_down``); the ranks'
-  outputs are summed, and only ``bias_rank`` keeps the bias;
-* or the whole group (``q_a``, ``kv``, replicated; never summed).
+* ``output``: an H128-aligned half of the output columns; the ranks' outputs
+  are concatenated in rank order;
+* ``input``: an H128-aligned half of the input channels; the ranks' outputs
+  are summed, so only ``bias_rank`` keeps the bias;
+* ``replicate``: the whole group.
 
-Weights stay compressed: the views slice the tiles (an output half repacks its
-trellis only when exported).  The input group must be a complete group of the
-site's shape -- a rank view is refused, so nothing is partitioned twice.
+Weights stay compressed (views of the tiles).  Only a complete group of the
+site's shape is accepted, so a rank view is never partitioned again.
 """
+from typing import NamedTuple
+
 import numpy as np
 
 from .loader import Exl3Tensor
 
-# site -> (input I, output N, partitioned axis, allowed whole-bit rates)
+
+class Site(NamedTuple):
+    inputs: int
+    outputs: int
+    axis: str           # "output", "input" or "replicate"
+    rates: tuple        # whole-bit rates the site's groups use
+
+
+# The partitioned model's sites (facts about the model, as the reference lists them).
 SITES = {
-    "q_b": (1280, 32768, "output", (4, 5)),
-    "o_b": (8192, 5120, "input", (4, 5)),
-    "shared_gate": (5120, 2304, "output", (4, 5)),
-    "shared_up": (5120, 2304, "output", (4, 5)),
-    "shared_down": (2304, 5120, "input", (4, 5)),
-    "q_a": (5120, 1280, "replicate", (4, 5)),
-    "kv": (5120, 512, "replicate", (4, 5)),
-    "expert_gate": (5120, 2304, "output", (2, 3)),
-    "expert_up": (5120, 2304, "output", (2, 3)),
-    "expert_down": (2304, 5120, "input", (2, 3)),
+    "q_b": Site(1280, 32768, "output", (4, 5)),
+    "o_b": Site(8192, 5120, "input", (4, 5)),
+    "shared_gate": Site(5120, 2304, "output", (4, 5)),
+    "shared_up": Site(5120, 2304, "output", (4, 5)),
+    "shared_down": Site(2304, 5120, "input", (4, 5)),
+    "q_a": Site(5120, 1280, "replicate", (4, 5)),
+    "kv": Site(5120, 512, "replicate", (4, 5)),
+    "expert_gate": Site(5120, 2304, "output", (2, 3)),
+    "expert_up": Site(5120, 2304, "output", (2, 3)),
+    "expert_down": Site(2304, 5120, "input", (2, 3)),
 }
 
 
-def _float_vector(value, size, itemsize):
-    return (isinstance(value, np.ndarray) and value.shape == (size,) and value.dtype.kind == "f"
-            and value.dtype.itemsize == itemsize and bool(np.isfinite(value).all()))
+def _is_vector(values, size, itemsize):
+    return (isinstance(values, np.ndarray) and values.dtype.kind == "f" and values.dtype.itemsize == itemsize
+            and values.shape == (size,) and bool(np.isfinite(values).all()))
 
 
-def _check(tensor, site):
+def _require_complete(tensor, name, site):
+    """The group is a whole, folded-scale mul1 group of the site's shape."""
     if not isinstance(tensor, Exl3Tensor):
-        raise ValueError("rank_partition requires an Exl3Tensor")
-    I, N, axis, rates = SITES[site]
-    if tensor.codebook != "mul1" or tensor.bits not in rates:
-        raise ValueError(f"{site} requires mul1 at bitrates {rates}")
+        raise ValueError("rank_partition takes an Exl3Tensor")
+    if tensor.codebook != "mul1" or tensor.bits not in site.rates:
+        raise ValueError(f"Site {name} takes mul1 groups at bitrates {site.rates}")
+    want = (site.inputs // 16, site.outputs // 16, 16 * int(tensor.bits))
     tr = tensor.trellis
-    if not isinstance(tr, np.ndarray) or tr.dtype.kind != "i" or tr.dtype.itemsize != 2 or \
-            tr.shape != (I // 16, N // 16, int(tensor.bits) * 16):
-        raise ValueError(f"{site} requires a complete I16 trellis for I={I}, N={N}")
-    if not _float_vector(tensor.suh, I, 2):
-        raise ValueError(f"Invalid folded F16 suh for {site}")
-    if not _float_vector(tensor.svh, N, 2):
-        raise ValueError(f"Invalid folded F16 svh for {site}")
-    if tensor.bias is not None and not _float_vector(tensor.bias, N, 4):
-        raise ValueError(f"Invalid F32 bias for {site}")
-    return I, N, axis
+    if not (isinstance(tr, np.ndarray) and tr.dtype.kind == "i" and tr.dtype.itemsize == 2 and tr.shape == want):
+        raise ValueError(f"Site {name} takes a complete I16 trellis of I={site.inputs}, N={site.outputs}")
+    checks = (("suh", tensor.suh, site.inputs, 2), ("svh", tensor.svh, site.outputs, 2))
+    for label, values, size, itemsize in checks:
+        if not _is_vector(values, size, itemsize):
+            raise ValueError(f"Site {name}: invalid folded F16 {label}")
+    if tensor.bias is not None and not _is_vector(tensor.bias, site.outputs, 4):
+        raise ValueError(f"Site {name}: invalid F32 bias")
 
 
 def rank_partition(tensor, site, rank, *, bias_rank=0):
-    """Rank `rank` (0 or 1) of a complete EXL3 group of TP site `site`."""
+    """Rank ``rank`` (0 or 1) of a complete EXL3 group of TP site ``site``."""
     if type(site) is not str or site not in SITES:
         raise ValueError("Unknown TP site")
-    if type(rank) is not int or rank not in (0, 1):
-        raise ValueError("rank must be the integer 0 or 1")
-    if type(bias_rank) is not int or bias_rank not in (0, 1):
-        raise ValueError("bias_rank must be the integer 0 or 1")
-    I, N, axis = _check(tensor, site)
-    if axis == "replicate":
-        return tensor
-    if axis == "output":
-        half = N // 2
+    for label, value in (("rank", rank), ("bias_rank", bias_rank)):
+        if type(value) is not int or value not in (0, 1):
+            raise ValueError(f"{label} must be the integer 0 or 1")
+    spec = SITES[site]
+    _require_complete(tensor, site, spec)
+    if spec.axis == "output":
+        half = spec.outputs // 2
         return tensor.slice_outputs(rank * half, (rank + 1) * half)
-    half = I // 2
-    return tensor.slice_inputs(rank * half, (rank + 1) * half, include_bias=rank == bias_rank)
+    if spec.axis == "input":
+        half = spec.inputs // 2
+        return tensor.slice_inputs(rank * half, (rank + 1) * half, include_bias=rank == bias_rank)
+    return tensor
