@@ -1,27 +1,35 @@
-// Prefill GEMM, wide variant for M >= 256: workgroup tile 256 x 256, eight
-// waves (two per SIMD) of 128 x 64, K stages of 64 channels, built on
+// Prefill GEMM, wide variant for M >= 256: workgroup tile 256 x BN, eight
+// waves (two per SIMD), K stages of 64 channels, built on
 // v_mfma_f32_32x32x16_f16.
 //
 // Measured on MI355X (independent accumulators, no memory traffic): the
 // 32x32x16 MFMA sustains ~2.1 PFLOP/s (85 % of the fp16 peak) with one or two
-// waves per SIMD, the 16x16x32 form only ~1.3-1.5 PFLOP/s; LDS reads run at
-// ~150 B/clk/CU.  So both operands are staged once per workgroup in LDS and
-// each wave computes a 128 x 64 block as 4 x 2 tiles of 32 x 32.  Per stage:
-//   * A (256 rows x 64 channels, 32 KiB) is DMA'd (buffer_load ... lds) from
-//     the 32x16 fragment-ordered core input straight into LDS, two stages
-//     ahead (three buffers);
-//   * B (64 x 256 = 4 input blocks x 16 tiles) is decoded from the trellis:
-//     wave w decodes block w / 2, tiles 8 (w % 2) .. +7, one chunk per lane,
-//     straight into 16x32 B-fragment order in LDS (double-buffered); the
-//     decode of stage st + 1 is interleaved with the MFMAs of stage st;
-//   * each wave runs 4 K16 steps x 4 x 2 v_mfma_f32_32x32x16_f16.
-// LDS: 3 A + 2 B buffers of 32 KiB; the epilogue reuses it as a [128][256]
-// FP32 tile (one half of the rows at a time) so each wave can run H128 over
-// whole 128-column groups.
+// waves per SIMD, the 16x16x32 form only ~1.3-1.5 PFLOP/s.  So both operands
+// are staged once per workgroup in LDS.  Per stage:
+//   * the core input (256 rows x 64 channels, 32 KiB) is DMA'd
+//     (buffer_load ... lds) from the 32x16 fragment-ordered workspace straight
+//     into LDS, two stages ahead (three buffers);
+//   * the weights (64 x BN = 4 input blocks x BN/16 tiles) are decoded from the
+//     trellis: wave w decodes one block's eight tiles, one chunk per lane,
+//     straight into 32x16 fragment order in LDS (double-buffered); the decode of
+//     stage st + 1 is interleaved with the MFMAs of stage st;
+//   * each wave multiplies its 128 output channels by its 64 (BN = 256) or 32
+//     (BN = 128) rows: 4 K16 steps x 4 x TM MFMAs.
+//
+// Operand roles: the decoded weights are the MFMA's A operand and the core
+// input its B operand, so the accumulators hold the transposed tile
+// D[channel][row].  A lane then holds 64 of the 128 channels of an output
+// H128 group for each of its rows (the other 64 in lane l ^ 32), and the
+// epilogue's Hadamard runs in registers: six butterfly levels between
+// registers and one through v_permlane32_swap, no LDS tile.
 //
 // MFMA 32x32x16 f16 operand layout (lane l, e = 0..7, r = 0..15), checked on
 // the device:  A: A[l % 32][8 (l / 32) + e]   B: B[8 (l / 32) + e][l % 32]
 //              D: D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
+// A weight fragment (k = 8 (l / 32) + e, column n = l % 32) and a core-input
+// fragment (row m = l % 32, k = 8 (l / 32) + e) therefore enter as A[n][k] and
+// B[k][m], and D[n][m] is output (row m, channel n): channel
+// 8 (r / 4) + 4 (l / 32) + r % 4 of the 32-channel tile, row l % 32.
 // Per output the K order is the MFMA K16 steps in ascending K from +0, as in
 // every other GEMM path here (the order inside one MFMA is the hardware's),
 // so rows have the same bits whichever tile computes them.
@@ -35,9 +43,13 @@ namespace stx {
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int WIDE_TILE_BYTES = 32 * 64 * 16;        // 32 fragments (8 x 4 K16) x 64 lanes x 16 B
-constexpr int WIDE_EPI_STRIDE = 260;                 // floats per staged row (256 + pad)
-constexpr size_t WIDE_LDS_BYTES =
-    5 * size_t(WIDE_TILE_BYTES) > 128 * WIDE_EPI_STRIDE * 4 ? 5 * size_t(WIDE_TILE_BYTES) : 128 * WIDE_EPI_STRIDE * 4;
+constexpr size_t WIDE_LDS_BYTES = 5 * size_t(WIDE_TILE_BYTES);
+
+// Bit casts through by-value parameters.  hipcc (ROCm 7.2) miscompiles
+// __builtin_bit_cast applied directly to an element of an ext_vector_type
+// value (it reads element 0), so vector elements pass through these.
+__device__ __forceinline__ uint32_t bits_of(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float float_of(uint32_t v) { return __builtin_bit_cast(float, v); }
 
 // Byte offset of the 32 x 16 A fragment (32-row block rb, 16-channel block kb) of lane l.
 __host__ __device__ __forceinline__ uint64_t afrag32_offset(uint32_t rb, uint32_t kb, uint32_t I, uint32_t lane) {
@@ -67,22 +79,25 @@ enum : int { kItemFull = 0, kItemHead = 1, kItemTail = 2 };
 // launch.
 constexpr uint32_t kHandoffForceRecompute = 0xFFFFFFFFu;   // poll_limit: always take over
 
-// BN = 256: 8 waves as 2 (M) x 4 (N), each 128 x 64 (4 x 2 MFMA tiles), all
-// eight decode.  BN = 128: 4 (M) x 2 (N), each 64 x 64 (2 x 2 tiles); the
-// stage's B is 8 tiles x 4 blocks, decoded by waves 0..3 (one per SIMD) while
-// waves 4..7 issue empty chunk loads so every wave counts the same vmcnt.
+// Each wave owns the 128 channels of one output H128 group and TM 32-row
+// blocks: BN = 256 as 4 (M) x 2 (N) waves of 64 rows, all eight decode;
+// BN = 128 as 8 (M) x 1 (N) waves of 32 rows, the stage's 8 tiles x 4 blocks
+// decoded by waves 0..3 (one per SIMD) while waves 4..7 issue empty chunk
+// loads so every wave counts the same vmcnt.
 template <int K, int CB, int BN, bool HANDOFF>
 __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     static_assert(!HANDOFF || BN == 256, "the handoff runs on 256 x 256 tiles");
-    constexpr int WNW = BN / 64;                         // waves along N
-    constexpr int TI = 256 / (8 / WNW) / 32;             // 32-row MFMA tiles per wave
-    constexpr int TJ = 2;                                // 32-column MFMA tiles per wave
+    static_assert(BN == 256 || BN == 128, "tile width");
+    constexpr int WN = BN / 128;                         // waves along N, one H128 group each
+    constexpr int TM = 256 / (8 / WN) / 32;              // 32-row MFMA tiles per wave
+    constexpr int TN = 4;                                // 32-channel MFMA tiles per wave
     constexpr int NT = BN / 16;                          // trellis tiles per stage row
     extern __shared__ __align__(16) unsigned char smem[];   // all 160 KiB: no static LDS besides
-    unsigned char* abuf = smem;                          // 3 x [8 rb32][4 kb16][64][16 B]
-    unsigned char* bbuf = smem + 3 * WIDE_TILE_BYTES;    // 2 x [BN/32 n32][4 kb16][64][16 B]
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int wm = w / WNW, wn = w % WNW;
+    unsigned char* abuf = smem;                          // 3 x [8 rb32][4 kb16][64][16 B] core input
+    unsigned char* bbuf = smem + 3 * WIDE_TILE_BYTES;    // 2 x [BN/32 n32][4 kb16][64][16 B] weights
+    // The wave index is uniform: readfirstlane keeps everything derived from it in SGPRs.
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = w / WN, wn = w % WN;
     const int jt8 = lane >> 3, g = lane & 7;
     const uint32_t I = a.I, N = a.N, stages = I / 64, half = stages / 2;
 
@@ -122,7 +137,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
 
     // Partial accumulators of split tile hslot: element e of wave w's lane l
     // at [hslot][w][e][l] (coalesced per element).
-    auto hpart = [&]() -> float* { return a.handoff + ((uint64_t(hslot) * 8 + w) * (TI * TJ * 16)) * 64 + lane; };
+    auto hpart = [&]() -> float* { return a.handoff + ((uint64_t(hslot) * 8 + w) * (TN * TM * 16)) * 64 + lane; };
 
     // K stages [s0, s_end) of this item.
     const uint32_t split = HANDOFF ? 0 : blockIdx.y;
@@ -165,7 +180,8 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     };
     // Lane (tile dtile, chunk g) holds rows 0..15 of tile columns g and g+8 of
     // input block dblk: column n = 16 (dtile % 2) + g (+8) of 32-column block
-    // dtile / 2; rows 0..7 go to fragment lane n, rows 8..15 to lane 32 + n.
+    // dtile / 2; rows 0..7 go to fragment lane n, rows 8..15 to lane 32 + n
+    // (the A-operand order A[n][k]).
     auto store_bfrag = [&](const half2_t (&wq)[4][4], int buf) {
         unsigned char* base = bbuf + buf * WIDE_TILE_BYTES + ((dtile >> 1) * 4 + dblk) * 1024;
         const int n = 16 * (dtile & 1) + g;
@@ -213,19 +229,20 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(v) : "memory");
     };
 
-    float16_t acc[TI][TJ];
+    // acc[jn][im]: channels 32 jn.. of the wave's group x rows 32 im.. of its block.
+    float16_t acc[TN][TM];
     if (!HANDOFF || s0 == 0) {
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+        for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) acc[i][j] = float16_t{};
+            for (int im = 0; im < TM; ++im) acc[jn][im] = float16_t{};
     } else {
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+        for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j)
+            for (int im = 0; im < TM; ++im)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = load_coherent(hpart() + ((i * TJ + j) * 16 + r) * 64);
+                for (int r = 0; r < 16; ++r) acc[jn][im][r] = load_coherent(hpart() + ((jn * TM + im) * 16 + r) * 64);
     }
 
     // Prologue: A stages s0 and s0 + 1 in flight, B stage s0 decoded, chunk ring full.
@@ -259,29 +276,26 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             if (decoder) link_chunk(dc, g == 0);
             half2_t wq[4][4];
             // Fragments of K16 step kb + 1 are read while step kb multiplies.
-            half8_t bf[2][TJ], af[2][TI];
+            half8_t wf[2][TN], xf[2][TM];
             auto read_frags = [&](int kb) {
 #pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    bf[kb & 1][j] = *reinterpret_cast<const half8_t*>(bb + (((TJ * wn + j) * 4 + kb) * 64 + lane) * 16);
+                for (int jn = 0; jn < TN; ++jn)
+                    wf[kb & 1][jn] = *reinterpret_cast<const half8_t*>(bb + (((TN * wn + jn) * 4 + kb) * 64 + lane) * 16);
 #pragma unroll
-                for (int i = 0; i < TI; ++i)
-                    af[kb & 1][i] = *reinterpret_cast<const half8_t*>(ab + (((TI * wm + i) * 4 + kb) * 64 + lane) * 16);
+                for (int im = 0; im < TM; ++im)
+                    xf[kb & 1][im] = *reinterpret_cast<const half8_t*>(ab + (((TM * wm + im) * 4 + kb) * 64 + lane) * 16);
             };
             read_frags(0);
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
                 if (kb < 3) read_frags(kb + 1);
 #pragma unroll
-                for (int i = 0; i < TI; ++i) {
+                for (int jn = 0; jn < TN; ++jn) {
 #pragma unroll
-                    for (int j = 0; j < TJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kb & 1][i], bf[kb & 1][j], acc[i][j], 0, 0, 0);
-                    // 16 weight pairs per stage, spread over the TI x 4 MFMA groups
-                    if (decoder) {
-#pragma unroll
-                        for (int q = 0; q < 4 / TI; ++q) decode_pair_at<K, CB>(dc, wq, 4 * kb + (4 / TI) * i + q);
-                    }
+                    for (int im = 0; im < TM; ++im)
+                        acc[jn][im] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[kb & 1][jn], xf[kb & 1][im], acc[jn][im], 0, 0, 0);
+                    // 16 weight pairs per stage, one after each of the 4 x 4 channel groups
+                    if (decoder) decode_pair_at<K, CB>(dc, wq, 4 * kb + jn);
                 }
             }
             // Decoded stage st + 1 -> the other B buffer (past the end: zeros
@@ -299,29 +313,41 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     // they land before LDS is reused as the epilogue tile or by the next item.
     stage_barrier(std::integral_constant<int, 0>{});
 
+    // Lane l holds rows 32 (TM wm + im) + l % 32 of the tile and, per MFMA
+    // tile jn and accumulator r, channel 32 jn + 8 (r / 4) + 4 (l / 32) + r % 4
+    // of the wave's group: four consecutive channels per (jn, r / 4), stored
+    // as one 16-byte access.  Row-major [rows][N] F32 outputs of the tile's 256
+    // rows go through a buffer resource sized to the rows below M, so accesses
+    // to rows >= M are dropped (stores) or read zeros (loads).
+    const uint32_t row0 = uint32_t(mb) * 256;
+    const uint32_t slab_bytes = (a.M - row0 < 256u ? a.M - row0 : 256u) * N * 4u;
+    const uint32_t out_off = ((32u * TM * wm + (lane & 31)) * N + uint32_t(BN) * c + 128u * wn + 4u * (lane >> 5)) * 4u;
+    auto acc4 = [&](int jn, int im, int r4) {
+        return u32x4{bits_of(acc[jn][im][4 * r4]), bits_of(acc[jn][im][4 * r4 + 1]), bits_of(acc[jn][im][4 * r4 + 2]),
+                     bits_of(acc[jn][im][4 * r4 + 3])};
+    };
+
     if (!HANDOFF && a.splits > 1) {
-        float* const plane = a.planes + uint64_t(split) * a.M * N;
+        const auto prsrc = make_rsrc(a.planes + (uint64_t(split) * a.M + row0) * N, slab_bytes);
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+        for (int im = 0; im < TM; ++im)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j)
+            for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t row = uint32_t(mb) * 256 + 32 * TI * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    const uint32_t col = uint32_t(BN) * c + 64 * wn + 32 * j + (lane & 31);
-                    if (row < a.M) plane[uint64_t(row) * N + col] = acc[i][j][r];
-                }
+                for (int r4 = 0; r4 < 4; ++r4)
+                    __builtin_amdgcn_raw_buffer_store_b128(acc4(jn, im, r4), prsrc, out_off + (32 * jn + 8 * r4) * 4,
+                                                           32 * im * N * 4, 0);
         return;
     }
 
     if (HANDOFF && kind == kItemHead) {
         float* const hp = hpart();
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+        for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j)
+            for (int im = 0; im < TM; ++im)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) store_coherent(hp + ((i * TJ + j) * 16 + r) * 64, acc[i][j][r]);
+                for (int r = 0; r < 16; ++r) store_coherent(hp + ((jn * TM + im) * 16 + r) * 64, acc[jn][im][r]);
         __builtin_amdgcn_s_waitcnt(0);   // every partial store complete
         __syncthreads();
         if (tid == 0) {
@@ -333,55 +359,127 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         return;
     }
 
-    // ---- Epilogue: rows [128 p, +128) through an LDS [128][BN] FP32 tile ----
-    // A wave always finishes column group w % (BN/128) of its rows, so its svh
-    // and bias operands are loaded once, ahead of the first pass.
-    constexpr int GROUPS = BN / 128;
-    const int grp = w % GROUPS;
-    const uint32_t n0 = uint32_t(BN) * c + 128u * grp + lane, n1 = n0 + 64;
-    const uint16_t sv0 = ld_global(a.svh + n0), sv1 = ld_global(a.svh + n1);
+    // ---- Epilogue: H128 per row in registers, then the output stage ----
+    // The tile's svh (and bias) go to LDS by DMA while the butterflies run:
+    // wave 0 brings BN x 2 B of svh to bytes [0, 1024), wave 1 BN x 4 B of
+    // bias to [1024, 2048) (lanes past the end read zeros).
     const bool has_bias = a.bias != nullptr;
-    const float b0 = has_bias ? ld_global(a.bias + n0) : 0.0f, b1 = has_bias ? ld_global(a.bias + n1) : 0.0f;
-    float* tile = reinterpret_cast<float*>(smem);
+    if (w < (has_bias ? 2 : 1)) {
+        const void* src = w == 0 ? static_cast<const void*>(a.svh + uint64_t(BN) * c)
+                                 : static_cast<const void*>(a.bias + uint64_t(BN) * c);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(src, w == 0 ? BN * 2 : BN * 4),
+                                                 (__attribute__((address_space(3))) void*)(smem + 1024 * w), 16,
+                                                 uint32_t(lane) * 16u, 0, 0, 0);
+    }
+    // Butterfly levels in the reference's order, channel bit 0 first; lower
+    // element a + b, upper element a - b.  Channel bits 0, 1, 3, 4 are bits of
+    // r, bits 5, 6 of jn, bit 2 is lane bit 5.  The values of one row block
+    // leave the accumulator tuples first (plain registers, no tuple copies).
+    auto bfly = [](float& lo, float& hi) {
+        const float x = lo, y = hi;
+        lo = x + y;
+        hi = x - y;
+    };
+    auto h128 = [&](auto imc, float (&v)[TN][16]) {
+        constexpr int im = decltype(imc)::value;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        if ((32 * TI * wm) / 128 == p) {
+        for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+            for (int r = 0; r < 16; ++r) v[jn][r] = acc[jn][im][r];
 #pragma unroll
-                for (int j = 0; j < TJ; ++j)
+        for (int jn = 0; jn < TN; ++jn) {
+            float* t = v[jn];
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int row = (32 * TI * wm) % 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        const int col = 64 * wn + 32 * j + (lane & 31);
-                        tile[row * WIDE_EPI_STRIDE + col] = acc[i][j][r];
-                    }
-        }
-        __syncthreads();
-        // 128 rows x GROUPS column groups; wave w takes rows w/GROUPS + RS q of
-        // group w % GROUPS, four rows per step with their butterflies interleaved.
-        constexpr int RS = 8 / GROUPS;
-        for (int r0 = w / GROUPS; r0 < 128; r0 += 4 * RS) {
-            float z0[4], z1[4];
+            for (int r = 0; r < 16; r += 2) bfly(t[r], t[r + 1]);                           // bit 0
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                z0[q] = tile[(r0 + RS * q) * WIDE_EPI_STRIDE + 128 * grp + lane];
-                z1[q] = tile[(r0 + RS * q) * WIDE_EPI_STRIDE + 128 * grp + lane + 64];
+            for (int r = 0; r < 16; ++r)
+                if (!(r & 2)) bfly(t[r], t[r + 2]);                                            // bit 1
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {                                                  // bit 2
+                // Swap the upper half of t[r] with the lower half of t[r + 1]:
+                // each lane then holds both bit-2 halves of one channel pair
+                // (lanes < 32: channel of t[r], lanes >= 32: of t[r + 1]);
+                // the same swap afterwards restores the layout.
+                const auto s1 = __builtin_amdgcn_permlane32_swap(bits_of(t[r]), bits_of(t[r + 1]), false, false);
+                const float x = float_of(s1[0]), y = float_of(s1[1]);
+                const auto s2 = __builtin_amdgcn_permlane32_swap(bits_of(x + y), bits_of(x - y), false, false);
+                t[r] = float_of(s2[0]);
+                t[r + 1] = float_of(s2[1]);
             }
-            h32_wave_multi<4>(z0, z1);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t row = uint32_t(mb) * 256 + 128 * p + r0 + RS * q;
-                if (row < a.M) {
-                    float* yr = a.y + uint64_t(row) * N;
-                    const float o0 = output_value(z0[q], sv0, has_bias, b0, a.alpha, a.beta, yr + n0);
-                    const float o1 = output_value(z1[q], sv1, has_bias, b1, a.alpha, a.beta, yr + n1);
-                    *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
-                    *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+            for (int r = 0; r < 16; ++r)
+                if (!(r & 4)) bfly(t[r], t[r + 4]);                                            // bit 3
+#pragma unroll
+            for (int r = 0; r < 8; ++r) bfly(t[r], t[r + 8]);                                  // bit 4
+            // One tile at a time: the scheduler's interleaving across tiles spills.
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            bfly(v[0][r], v[1][r]);                                                            // bit 5
+            bfly(v[2][r], v[3][r]);
+#pragma unroll
+            for (int jn = 0; jn < 2; ++jn) {                                                   // bit 6, scaled
+                const float x = v[jn][r], y = v[jn + 2][r];
+                v[jn][r] = (x + y) * INV_SQRT128;   // (a + b) * c: nothing to contract
+                v[jn + 2][r] = (x - y) * INV_SQRT128;
+            }
+        }
+    };
+
+    // Output stage per element, as output_value() with the operands in
+    // registers: RN32(h * svh), + bias, * alpha, + RN32(beta * y).  A missing
+    // bias adds -0.0, which leaves every value (signed zeros included)
+    // unchanged; y is read only when beta != 0.
+    const uint16_t* sv_lds = reinterpret_cast<const uint16_t*>(smem);
+    const float* bias_lds = reinterpret_cast<const float*>(smem + 1024);
+    const uint32_t lc0 = 128u * wn + 4u * (lane >> 5);   // first channel of the lane within the tile
+    const auto yrsrc = make_rsrc(a.y + uint64_t(row0) * N, slab_bytes);
+    auto emit = [&](auto imc, const float (&v)[TN][16], auto with_beta) {
+        constexpr int im = decltype(imc)::value;
+        constexpr bool BETA = decltype(with_beta)::value;
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const uint32_t lc = lc0 + 32 * jn + 8 * r4;
+                const uint2 sv = *reinterpret_cast<const uint2*>(sv_lds + lc);
+                const float4_t bv = has_bias ? *reinterpret_cast<const float4_t*>(bias_lds + lc)
+                                             : float4_t{-0.0f, -0.0f, -0.0f, -0.0f};
+                const uint32_t sw[4] = {sv.x & 0xFFFFu, sv.x >> 16, sv.y & 0xFFFFu, sv.y >> 16};
+                const uint32_t off = out_off + (32 * jn + 8 * r4) * 4;
+                u32x4 old{};
+                if constexpr (BETA) old = __builtin_amdgcn_raw_buffer_load_b128(yrsrc, off, 32 * im * N * 4, 0);
+                u32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float y = rn32(v[jn][4 * r4 + e] * half_bits_to_float(uint16_t(sw[e])));
+                    y = rn32(y + bv[e]);
+                    y = rn32(y * a.alpha);
+                    if constexpr (BETA) y = rn32(y + rn32(a.beta * float_of(old[e])));
+                    o[e] = bits_of(y);
                 }
+                __builtin_amdgcn_raw_buffer_store_b128(o, yrsrc, off, 32 * im * N * 4, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
-        }
-        __syncthreads();
+    };
+    // Row block by row block: each one's results are stored before the next
+    // one's butterflies, which bounds the live values.
+    const bool use_beta = a.beta != 0.0f;
+    auto emit_any = [&](auto imc, const float (&v)[TN][16]) {
+        if (use_beta) emit(imc, v, std::true_type{});
+        else emit(imc, v, std::false_type{});
+    };
+    float v[TN][16];
+    constexpr std::integral_constant<int, 0> first{};
+    h128(first, v);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's svh / bias DMA landed
+    __syncthreads();
+    emit_any(first, v);
+    if constexpr (TM == 2) {
+        constexpr std::integral_constant<int, 1> second{};
+        h128(second, v);
+        emit_any(second, v);
     }
 }
 

@@ -103,7 +103,11 @@ WideSplit wide_split(uint64_t m, const DeviceWeights& w) {
     return {uint32_t(nc), 0};
 }
 
-bool gemm_wide(uint64_t m, const DeviceWeights& w) { return m >= 256 && w.output % 256 == 0; }
+// The wide kernel addresses each 256-row slab of its output (256 x N x 4
+// bytes) through one buffer resource, so N stays below 2^22.
+bool gemm_wide(uint64_t m, const DeviceWeights& w) {
+    return m >= 256 && w.output % 256 == 0 && w.output < (1u << 22);
+}
 
 // K split of a wide pass (no handoff) whose workgroups fill at most half of
 // the 256 CUs, e.g. M = 256..768 on 5120^2 (20 to 60 tiles): S workgroups per
