@@ -545,6 +545,10 @@ def run_section(ctx, which, steps, warmup):
     cells = []
     if which == "gemv":
         cells.append(bench_gemv(ctx, 4096, 4096, 4, 1, steps, warmup, synth.BASE_SEED))
+        for (I, N) in ((5120, 5120), (4096, 12288)):
+            for K in (4, 5, 6):
+                for R in (1, 2, 4, 8):
+                    cells.append(bench_gemv(ctx, I, N, K, R, small_steps, small_warm, synth.BASE_SEED + 1))
     elif which == "gemm":
         for (I, N) in ((4096, 12288), (5120, 5120)):
             for K in (4, 5, 6):

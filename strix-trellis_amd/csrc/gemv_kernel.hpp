@@ -15,8 +15,10 @@
 //     ring are issued before it so their latency overlaps it;
 //   * main loop: wave w takes input blocks w, w+4, ...; per block every lane
 //     loads its K-word chunk (K*256 contiguous bytes per wave), decodes 32
-//     weights in VGPRs and runs, per row, two v_dot2 chains (columns g, g+8)
-//     against activation pairs read from LDS by broadcast;
+//     weights in VGPRs, moves them into matrix-core operand order with eight
+//     v_permlane32_swap and multiplies them with the block's activations (read
+//     from LDS by broadcast) in 8 or 16 v_mfma_f32_4x4x4_16b_f16, whatever the
+//     row count up to four or eight;
 //   * the four waves' partial sums meet in LDS and are added in wave order;
 //   * S == 1: the workgroup applies the output stage itself.  Otherwise it
 //     writes its [rows][128] partial plane; the finishing step (a second
@@ -26,8 +28,8 @@
 //
 // Per-output accumulation order (defines the core's bits; depends on I, N,
 // K only, never on the row count):
-//   lane chain  : +0, then blocks in ascending order; within a block the dot2
-//                 pairs (rows 2V,2V+1) then (2V+8,2V+9) for V = 0..3;
+//   lane chain  : +0, then blocks in ascending order; within a block the four
+//                 K steps of four input rows (one MFMA product sum each);
 //   wave fold   : chain(w0) + chain(w1) + chain(w2) + chain(w3);
 //   split fold  : ((+0 + P0) + P1) + ... + P(S-1).
 #pragma once
@@ -268,36 +270,93 @@ __device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeig
         __hip_atomic_store(a.state.epochs + cz, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The block activations of every row, read from LDS ahead of the decode (up
-// to four rows, 8 VGPRs each): the decode hides their LDS round trip, which
-// the compiler otherwise places, and waits for, right before the dots
-// (C1 8.26 -> 8.19 us, 5120^2 R1 12.9 -> 12.6 us).
+// ---------------------------------------------------------------------------
+// Matrix-core dot: v_mfma_f32_4x4x4_16b_f16, sixteen 4x4x4 products per
+// instruction.  Operand layout, checked on the device: block b uses lanes
+// 4b..4b+3; A[b][i][k] sits in lane 4b+i, B[b][k][j] in lane 4b+j (halves
+// k = 0..3), D[b][i][j] in lane 4b+j, element i.  Here A is 64 weight
+// columns (A row = lane), B the activations of four rows, D their products.
+//
+// A decoded chunk (lane 8t+g holds columns g and g+8 of tile t, input rows
+// 0..15 of the block: wq[V][khalf + 2 sel], sel selecting column g + 8 sel)
+// becomes the A operands by one v_permlane32_swap per register pair
+// (sel 0, sel 1): the first register then holds tiles 0..3 and the second
+// tiles 4..7 (half h = 0, 1), with lane bit 5 selecting the column.  So A row
+// p of half h is output column
+//   chan(p, h) = 16 ((p >> 3) & 3) + 8 (p >> 5) + (p & 7) + 64 h,
+// and K step q (block rows 4q..4q+3) of half h is wq[2 (q & 1)][q / 2 + 2 h]
+// followed by wq[2 (q & 1) + 1][q / 2 + 2 h].  B (step q, row quad rh): lane l
+// reads activation row 4 rh + l % 4, clamped to RT - 1 (a D column of a row
+// past RT is never read), block rows 4q..4q+3.
+// Per output: +0, then blocks in ascending order, within a block K steps
+// q = 0..3 (four products each, in the hardware's order).  D columns are
+// independent, so a row's bits do not depend on the other rows.
+// ---------------------------------------------------------------------------
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float gemv_f4_t __attribute__((ext_vector_type(4)));
+
 template <int RT>
-__device__ __forceinline__ void load_act_block(const _Float16* act, uint32_t act_row, u32x4 (&xv)[RT][2]) {
+struct MfmaAcc {
+    static constexpr int RH = (RT + 3) / 4;   // row quads
+    gemv_f4_t d[2][RH];                        // [half h][row quad]
+};
+
+template <int RT>
+__device__ __forceinline__ void mfma_acc_zero(MfmaAcc<RT>& acc) {
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(act + r * act_row);
-        xv[r][0] = p[0];
-        xv[r][1] = p[1];
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int rh = 0; rh < MfmaAcc<RT>::RH; ++rh) acc.d[h][rh] = gemv_f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 }
+
+__device__ __forceinline__ half4_t join_h4(half2_t lo, half2_t hi) { return half4_t{lo.x, lo.y, hi.x, hi.y}; }
+
+// One decoded block (wq, consumed) against the activations `act` of its 16
+// input rows (act + r * act_row: activation row r).
 template <int RT>
-__device__ __forceinline__ void dot_block_x(const half2_t (&wq)[4][4], const u32x4 (&xv)[RT][2], float (&acc)[RT][2]) {
+__device__ __forceinline__ void mfma_dot_block(half2_t (&wq)[4][4], const _Float16* act, uint32_t act_row,
+                                               MfmaAcc<RT>& acc) {
+    constexpr int RH = MfmaAcc<RT>::RH;
+    const int lane = threadIdx.x & 63;
+    half4_t xb[4][RH];
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-        const u32x4 lo = xv[r][0], hi = xv[r][1];
-        const half2_t xp[8] = {as_h2(lo.x), as_h2(lo.y), as_h2(lo.z), as_h2(lo.w),
-                               as_h2(hi.x), as_h2(hi.y), as_h2(hi.z), as_h2(hi.w)};
-        float a0 = acc[r][0], a1 = acc[r][1];
+    for (int rh = 0; rh < RH; ++rh) {
+        const int row = 4 * rh + (lane & 3) < RT ? 4 * rh + (lane & 3) : RT - 1;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            a0 = __builtin_amdgcn_fdot2(wq[v][0], xp[v], a0, false);
-            a0 = __builtin_amdgcn_fdot2(wq[v][1], xp[v + 4], a0, false);
-            a1 = __builtin_amdgcn_fdot2(wq[v][2], xp[v], a1, false);
-            a1 = __builtin_amdgcn_fdot2(wq[v][3], xp[v + 4], a1, false);
+        for (int q = 0; q < 4; ++q) xb[q][rh] = *reinterpret_cast<const half4_t*>(act + row * act_row + 4 * q);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(as_u32(wq[v][kh]), as_u32(wq[v][kh + 2]), false, false);
+            wq[v][kh] = as_h2(sw[0]);
+            wq[v][kh + 2] = as_h2(sw[1]);
         }
-        acc[r][0] = a0;
-        acc[r][1] = a1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const half4_t av = join_h4(wq[2 * (q & 1)][q / 2 + 2 * h], wq[2 * (q & 1) + 1][q / 2 + 2 * h]);
+#pragma unroll
+            for (int rh = 0; rh < RH; ++rh)
+                acc.d[h][rh] = __builtin_amdgcn_mfma_f32_4x4x4f16(av, xb[q][rh], acc.d[h][rh], 0, 0, 0);
+        }
+}
+
+// The wave's sums to `red` ([RT][128] F32, row-major): lane 4b+j holds row
+// 4 rh + j, columns chan(4b + i, h) for i = 0..3, four consecutive columns.
+template <int RT>
+__device__ __forceinline__ void mfma_partials(const MfmaAcc<RT>& acc, float* red) {
+    const int lane = threadIdx.x & 63, b = lane >> 2;
+    const int ch0 = 4 * (b & 1) + 16 * ((b >> 1) & 3) + 8 * (b >> 3);
+#pragma unroll
+    for (int rh = 0; rh < MfmaAcc<RT>::RH; ++rh) {
+        const int row = 4 * rh + (lane & 3);
+        if (row < RT) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) *reinterpret_cast<gemv_f4_t*>(red + row * 128 + ch0 + 64 * h) = acc.d[h][rh];
+        }
     }
 }
 
@@ -373,19 +432,39 @@ void gemv_kernel(GemvArgs a) {
     const uint32_t epoch = fused ? load_epoch(a.state.epochs + place.cz) : 0u;
 
     // Prologue: FP16 core input of this split's channels, one 128-block unit
-    // per wave.  The first two units' loads are issued before the weight
-    // prefetch, so waiting for them does not wait for the weights.
+    // per wave at a time, the loads of kUnits units per wave in flight
+    // together (each batch is one memory round trip; one unit at a time made
+    // the 8-row input stage six round trips long).  The first batch is issued
+    // before the weight prefetch, so waiting for it does not wait for the
+    // weights.  (Four units in flight make the 3- and 4-row mcg / 3inst
+    // kernels spill, so those keep two.)
+    constexpr int kUnits = RT <= 2 ? 2 : RT <= 4 ? (CB == CB_MUL1 ? 4 : 2) : 8;
     const int hblocks = a.bps / 8, units = RT * hblocks;
+    // Unit u is row u % RT of 128-block u / RT (constant divisors).
     auto unit_load = [&](int u) -> InputLoad {
-        const int r = u / hblocks, hb = u % hblocks;
+        const int r = u % RT, hb = u / RT;
         const uint32_t ch = a0 * 16 + hb * 128;
         const bool live = uint32_t(r) < a.rows;
         return input_load(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, live);
     };
-    auto unit_out = [&](int u) -> _Float16* { return act + (u / hblocks) * act_row + (u % hblocks) * 128; };
+    auto unit_out = [&](int u) -> _Float16* { return act + (u % RT) * act_row + (u / RT) * 128; };
     // Units past the end load unit 0 again (valid addresses, result unused).
-    const InputLoad pre0 = unit_load(w < units ? w : 0);
-    const InputLoad pre1 = unit_load(w + GEMV_WAVES < units ? w + GEMV_WAVES : 0);
+    auto batch_load = [&](int u0, InputLoad (&l)[kUnits]) {
+#pragma unroll
+        for (int i = 0; i < kUnits; ++i) {
+            const int u = u0 + GEMV_WAVES * i;
+            l[i] = unit_load(u < units ? u : 0);
+        }
+    };
+    auto batch_compute = [&](int u0, const InputLoad (&l)[kUnits]) {
+#pragma unroll
+        for (int i = 0; i < kUnits; ++i) {
+            const int u = u0 + GEMV_WAVES * i;
+            if (u < units) input_compute(l[i], unit_out(u));
+        }
+    };
+    InputLoad pre[kUnits];
+    batch_load(w, pre);
     __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the weight prefetch
 
     Chunk<K> ring[4];
@@ -395,46 +474,34 @@ void gemv_kernel(GemvArgs a) {
     // The chunks stay in their registers across the input stage: decoding
     // blocks ahead of the barrier (to overlap the input loads) was measured
     // slower, the decoded weights holding 32 more VGPRs per lane.
-    if (w < units) input_compute(pre0, unit_out(w));
-    if (w + GEMV_WAVES < units) input_compute(pre1, unit_out(w + GEMV_WAVES));
-    for (int u = w + 2 * GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
+    batch_compute(w, pre);
+    for (int u0 = w + kUnits * GEMV_WAVES; u0 < units; u0 += kUnits * GEMV_WAVES) {
+        InputLoad l[kUnits];
+        batch_load(u0, l);
+        batch_compute(u0, l);
+    }
     __syncthreads();
 
     const bool first = g == 0;
-    float acc[RT][2];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+    MfmaAcc<RT> acc;
+    mfma_acc_zero(acc);
     // Slot t % 4 holds block t; it is refilled with block t + 4.
     for (int t = 0; t < nb; t += 4) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             Chunk<K>& slot = ring[u];
             if (t + u < nb) {
-                if constexpr (RT <= 4) {
-                    u32x4 xv[RT][2];
-                    load_act_block<RT>(act + (w + GEMV_WAVES * (t + u)) * 16, act_row, xv);
-                    __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the decode
-                    half2_t wq[4][4];
-                    link_chunk(slot, first);
-                    decode_chunk<K, CB>(slot, wq);
-                    dot_block_x<RT>(wq, xv, acc);
-                } else {
-                    half2_t wq[4][4];
-                    link_chunk(slot, first);
-                    decode_chunk<K, CB>(slot, wq);
-                    dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
-                }
+                half2_t wq[4][4];
+                link_chunk(slot, first);
+                decode_chunk<K, CB>(slot, wq);
+                mfma_dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
             }
             load_chunk(slot, rsrc, block_off(t + u + 4));
         }
     }
 
     // Wave partials -> LDS, added in wave order.
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-        red[(w * RT + r) * 128 + 16 * jt + g] = acc[r][0];
-        red[(w * RT + r) * 128 + 16 * jt + g + 8] = acc[r][1];
-    }
+    mfma_partials<RT>(acc, red + w * RT * 128);
     lds_barrier();
     float* cur = fused ? fused_planes(a, place.cz, epoch & 1u) : nullptr;
     float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
@@ -517,9 +584,8 @@ __global__ __launch_bounds__(OWNER_THREADS) void gemv_owner_kernel(GemvArgs a) {
     for (uint32_t s0 = 0; s0 < a.splits; s0 += OWNER_GROUPS) {
         const uint32_t s = s0 + uint32_t(grp);
         const bool active = s < a.splits;
-        float acc[RT][2];
-#pragma unroll
-        for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+        MfmaAcc<RT> acc;
+        mfma_acc_zero(acc);
         Chunk<K> ring[4];
         const uint32_t a0 = (active ? s : s0) * a.bps;
         const auto rsrc = make_rsrc(reinterpret_cast<const char*>(gw.trellis) + uint64_t(a0) * row_bytes,
@@ -552,21 +618,14 @@ __global__ __launch_bounds__(OWNER_THREADS) void gemv_owner_kernel(GemvArgs a) {
                         half2_t wq[4][4];
                         link_chunk(slot, first);
                         decode_chunk<K, CB>(slot, wq);
-                        dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+                        mfma_dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
                     }
                     load_chunk(slot, rsrc, block_off(t + u + 4));
                 }
             }
         }
         __syncthreads();   // every group's dots are done: the partials may overwrite the inputs
-        if (active) {
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                float* rr = red + ((grp * GEMV_WAVES + w) * RT + r) * 128;
-                rr[16 * jt + g] = acc[r][0];
-                rr[16 * jt + g + 8] = acc[r][1];
-            }
-        }
+        if (active) mfma_partials<RT>(acc, red + (grp * GEMV_WAVES + w) * RT * 128);
         __syncthreads();
         if (tid < RT * 128) {
             const int r = tid >> 7, n = tid & 127;
