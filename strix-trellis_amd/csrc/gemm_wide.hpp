@@ -135,9 +135,14 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     const int c = t % a.col_blocks + a.col_block0, mb = t / a.col_blocks;   // c: BN-column block
     const uint32_t lane_off = (uint32_t(NT) * c + dtile) * tile_bytes + g * 4u * K;
 
-    // Partial accumulators of split tile hslot: element e of wave w's lane l
-    // at [hslot][w][e][l] (coalesced per element).
-    auto hpart = [&]() -> float* { return a.handoff + ((uint64_t(hslot) * 8 + w) * (TN * TM * 16)) * 64 + lane; };
+    // Partial accumulators of split tile hslot, 256 KiB per tile: elements
+    // 4q .. 4q+3 of wave w's lane l at [hslot][w][q][l][4], one 16-byte
+    // device-coherent (sc1) access per lane and quad, 1 KiB contiguous per
+    // wave; quad q = (jn TM + im) 4 + r / 4.  (One 4-byte access per element
+    // made the handoff's partial traffic the slower part of a split tile.)
+    constexpr int kCoherent = 16;   // buffer cache policy bits: sc1
+    const auto hrsrc = make_rsrc(a.handoff + uint64_t(hslot) * (8u * TN * TM * 16 * 64), 8u * TN * TM * 16 * 64 * 4);
+    auto quad_off = [&](int q) { return uint32_t(((w * (TN * TM * 4) + q) * 64 + lane) * 16); };
 
     // K stages [s0, s_end) of this item.
     const uint32_t split = HANDOFF ? 0 : blockIdx.y;
@@ -242,7 +247,12 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
 #pragma unroll
             for (int im = 0; im < TM; ++im)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[jn][im][r] = load_coherent(hpart() + ((jn * TM + im) * 16 + r) * 64);
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(hrsrc, quad_off((jn * TM + im) * 4 + r4), 0,
+                                                                          kCoherent);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[jn][im][4 * r4 + e] = float_of(v[e]);
+                }
     }
 
     // Prologue: A stages s0 and s0 + 1 in flight, B stage s0 decoded, chunk ring full.
@@ -341,13 +351,14 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     }
 
     if (HANDOFF && kind == kItemHead) {
-        float* const hp = hpart();
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
             for (int im = 0; im < TM; ++im)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) store_coherent(hp + ((jn * TM + im) * 16 + r) * 64, acc[jn][im][r]);
+                for (int r4 = 0; r4 < 4; ++r4)
+                    __builtin_amdgcn_raw_buffer_store_b128(acc4(jn, im, r4), hrsrc, quad_off((jn * TM + im) * 4 + r4), 0,
+                                                           kCoherent);
         __builtin_amdgcn_s_waitcnt(0);   // every partial store complete
         __syncthreads();
         if (tid == 0) {

@@ -2,8 +2,8 @@
 // with the ordered score-weighted top-k fold.
 //
 // Both launches reuse the GEMV building blocks (in-register trellis decode,
-// v_dot2 chains, LDS wave fold, coherent partial planes, last-arrival finish)
-// with routed rows instead of a fixed row range:
+// the matrix-core dot, LDS wave fold, coherent partial planes, last-arrival
+// finish) with routed rows instead of a fixed row range:
 //
 //   gate/up : grid (H/128, s_gu, rows*k), 256 threads.  Workgroup (c, s, r)
 //             takes the r-th expert group (its leader is the first valid
@@ -21,9 +21,10 @@
 //             finishes alpha/beta.  Invalid tokens get NaN rows.
 //
 // Accumulation order per projection (fixes the bits; independent of which
-// other tokens are routed to the same expert): lane chain over the wave's
-// blocks w, w+4, ... in ascending order; wave fold 0..3; split fold ascending
-// from +0 — the GEMV order of the same split decomposition.
+// other tokens are routed to the same expert): over the wave's blocks w,
+// w+4, ... in ascending order, four MFMA K steps per block; wave fold 0..3;
+// split fold ascending from +0 — the GEMV order of the same split
+// decomposition.
 #pragma once
 #include "moe.hpp"
 #include "gemv_kernel.hpp"
@@ -96,8 +97,7 @@ struct MoeGroup {
 // first and spread evenly over the CUs, instead of sitting wherever their
 // routes happen to lead.  Ranks past the groups take the
 // invalid tokens in order (there are at least as many: an invalid token's k
-// routes lead nothing).  One lane per route; every wave resolves for itself, so
-// the result stays in registers and no barrier is needed to share it.
+// routes lead nothing).  One lane per route, in one wave (moe_group_shared).
 //
 // Groups are enumerated in leader order: each pass takes the lowest valid
 // route not yet grouped -- it leads its expert's group, since every lower
@@ -154,6 +154,30 @@ __device__ __forceinline__ const char* moe_first_ptr(const uint32_t* p) {
 __device__ __forceinline__ MoeGroup moe_uniform(const MoeGroup& g) {
     return {moe_first(g.members), moe_first(g.active), moe_first(g.expert), moe_first(g.route),
             moe_first(uint32_t(g.leader)) != 0, int(moe_first(uint32_t(g.nan_row)))};
+}
+
+// The group of the workgroup (rank = grid z): wave 0 resolves it and shares
+// it through LDS (`slot`, 8 words), one barrier instead of four resolutions,
+// each a few hundred issue slots of a CU that the decode keeps busy.
+__device__ __forceinline__ MoeGroup moe_group_shared(const MoeArgs& a, uint32_t rank, uint32_t* slot) {
+    if (threadIdx.x < 64) {
+        const MoeGroup g = moe_uniform(moe_resolve(a, rank));
+        if (threadIdx.x == 0) {
+            slot[0] = uint32_t(g.members);
+            slot[1] = uint32_t(g.members >> 32);
+            slot[2] = uint32_t(g.active);
+            slot[3] = uint32_t(g.active >> 32);
+            slot[4] = g.expert;
+            slot[5] = g.route;
+            slot[6] = uint32_t(g.leader);
+            slot[7] = uint32_t(g.nan_row);
+        }
+    }
+    __syncthreads();
+    const volatile uint32_t* v = slot;
+    const MoeGroup g = {uint64_t(v[0]) | (uint64_t(v[1]) << 32), uint64_t(v[2]) | (uint64_t(v[3]) << 32), v[4], v[5],
+                        v[6] != 0, int(v[7])};
+    return moe_uniform(g);
 }
 
 // Fold `splits` planes of two sets p and q (stride between splits `step`
@@ -218,6 +242,37 @@ constexpr int MOE_D_ACT_BYTES = MOE_MAX_RT * MOE_D_MAX_BPS * 16 * 2;
 constexpr int MOE_D_RED_BYTES = GEMV_WAVES * MOE_MAX_RT * 128 * 4;
 constexpr int moe_max(int a, int b) { return a > b ? a : b; }
 
+// Input-stage units of a wave (u = w, w + 4, ...) in batches of MOE_UNITS
+// whose loads are in flight together, one memory round trip per batch.
+// Units past the end load unit 0 again (valid addresses, result unused).
+constexpr int MOE_UNITS = 4;
+template <class Load>
+__device__ __forceinline__ void moe_batch_load(int u0, int units, InputLoad (&l)[MOE_UNITS], Load load) {
+#pragma unroll
+    for (int i = 0; i < MOE_UNITS; ++i) {
+        const int u = u0 + GEMV_WAVES * i;
+        l[i] = load(u < units ? u : 0);
+    }
+}
+// Computes the batch loaded in `pre` (units from w), then the wave's other units.
+template <class Load, class Out>
+__device__ __forceinline__ void moe_input_stage(int w, int units, const InputLoad (&pre)[MOE_UNITS], Load load,
+                                                Out out) {
+    auto compute = [&](int u0, const InputLoad (&l)[MOE_UNITS]) {
+#pragma unroll
+        for (int i = 0; i < MOE_UNITS; ++i) {
+            const int u = u0 + GEMV_WAVES * i;
+            if (u < units) input_compute(l[i], out(u));
+        }
+    };
+    compute(w, pre);
+    for (int u0 = w + MOE_UNITS * GEMV_WAVES; u0 < units; u0 += MOE_UNITS * GEMV_WAVES) {
+        InputLoad l[MOE_UNITS];
+        moe_batch_load(u0, units, l, load);
+        compute(u0, l);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Gate/up core of one workgroup: NP = 2 projections sharing the routed rows.
 // ---------------------------------------------------------------------------
@@ -239,9 +294,10 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
     auto offu = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbu + ou : kOut; };
 
     // Input stages (gate and up have their own suh): one 128-block per wave and
-    // unit.  The wave's first two units are loaded before the weight prefetch:
-    // vector loads complete in issue order, so loads issued after the chunks
-    // would wait for the chunks' HBM round trip.
+    // unit, the loads of MOE_UNITS units per wave in flight together.  The
+    // first batch is loaded before the weight prefetch: vector loads complete
+    // in issue order, so loads issued after the chunks would wait for the
+    // chunks' HBM round trip.
     const int hblocks = int(bps) / 8, per_proj = nrows * hblocks, units = 2 * per_proj;
     auto unit_load = [&](int u) -> InputLoad {
         const int p = u / per_proj, v = u - p * per_proj;
@@ -256,9 +312,8 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
         const int i = v / hblocks, hb = v - i * hblocks;
         return act + (p * MOE_MAX_RT + i) * act_row + hb * 128;
     };
-    // Units past the end load unit 0 again (valid addresses, result unused).
-    const InputLoad pre0 = unit_load(w < units ? w : 0);
-    const InputLoad pre1 = unit_load(w + GEMV_WAVES < units ? w + GEMV_WAVES : 0);
+    InputLoad pre[MOE_UNITS];
+    moe_batch_load(w, units, pre, unit_load);
     __builtin_amdgcn_sched_barrier(0);
 
     Chunk<KG> cg[MOE_RING_GU];
@@ -269,17 +324,15 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
         load_chunk(cu[u], ru, offu(u));
     }
 
-    if (w < units) input_compute(pre0, unit_out(w));
-    if (w + GEMV_WAVES < units) input_compute(pre1, unit_out(w + GEMV_WAVES));
-    for (int u = w + 2 * GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
-    // Rows past nrows stay unused: dot_block reads only rows < RT and the
-    // fold below only rows < nrows; rows nrows..RT-1 hold stale LDS and their
-    // sums are discarded.
+    moe_input_stage(w, units, pre, unit_load, unit_out);
+    // Rows past nrows stay unused: rows nrows..RT-1 hold stale LDS, their
+    // columns of the products are independent of the others, and the fold
+    // below reads only rows < nrows.
     __syncthreads();
 
-    float accg[RT][2], accu[RT][2];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) accg[r][0] = accg[r][1] = accu[r][0] = accu[r][1] = 0.0f;
+    MfmaAcc<RT> accg, accu;
+    mfma_acc_zero(accg);
+    mfma_acc_zero(accu);
     const bool first = g == 0;
     for (int t = 0; t < nb; t += MOE_RING_GU) {
 #pragma unroll
@@ -289,23 +342,18 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
                 half2_t wq[4][4];
                 link_chunk(cg[u], first);
                 decode_chunk<KG, CB_MUL1>(cg[u], wq);
-                dot_block<RT>(wq, act + blk * 16, act_row, accg);
+                mfma_dot_block<RT>(wq, act + blk * 16, act_row, accg);
                 link_chunk(cu[u], first);
                 decode_chunk<KU, CB_MUL1>(cu[u], wq);
-                dot_block<RT>(wq, act + MOE_MAX_RT * act_row + blk * 16, act_row, accu);
+                mfma_dot_block<RT>(wq, act + MOE_MAX_RT * act_row + blk * 16, act_row, accu);
             }
             load_chunk(cg[u], rg, offg(t + u + MOE_RING_GU));
             load_chunk(cu[u], ru, offu(t + u + MOE_RING_GU));
         }
     }
     __syncthreads();   // every wave is done with act before red overwrites it
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-        red[((w * 2 + 0) * MOE_MAX_RT + r) * 128 + 16 * jt + g] = accg[r][0];
-        red[((w * 2 + 0) * MOE_MAX_RT + r) * 128 + 16 * jt + g + 8] = accg[r][1];
-        red[((w * 2 + 1) * MOE_MAX_RT + r) * 128 + 16 * jt + g] = accu[r][0];
-        red[((w * 2 + 1) * MOE_MAX_RT + r) * 128 + 16 * jt + g + 8] = accu[r][1];
-    }
+    mfma_partials<RT>(accg, red + (w * 2 + 0) * MOE_MAX_RT * 128);
+    mfma_partials<RT>(accu, red + (w * 2 + 1) * MOE_MAX_RT * 128);
     __syncthreads();
 }
 
@@ -322,9 +370,10 @@ void moe_gate_up_kernel(MoeArgs a) {
     __shared__ __align__(16) unsigned char lds[moe_max(MOE_GU_ACT_BYTES, MOE_GU_RED_BYTES)];
     _Float16* act = reinterpret_cast<_Float16*>(lds);
     float* red = reinterpret_cast<float*>(lds);
+    __shared__ uint32_t group_slot[8];
     const uint32_t c = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6;
-    const MoeGroup grp = moe_uniform(moe_resolve(a, blockIdx.z));
+    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot);
     if (!grp.leader || !grp.active) return;
     const uint32_t route = grp.route;
     const uint64_t active = grp.active;
@@ -400,7 +449,7 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
     constexpr uint32_t kOut = 0x80000000u;
     auto off = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rb + lo : kOut; };
 
-    // Input stage of the hidden rows; the wave's first two units are loaded
+    // Input stage of the hidden rows; the first batch of units is loaded
     // ahead of the weight prefetch (see the gate/up core).
     const int hblocks = int(bps) / 8, units = nrows * hblocks;
     auto unit_load = [&](int u) -> InputLoad {
@@ -410,22 +459,19 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
         return input_load(a.hidden + uint64_t(j) * a.H + ch, ex.down.suh + ch, true);
     };
     auto unit_out = [&](int u) -> _Float16* { return act + (u / hblocks) * act_row + (u % hblocks) * 128; };
-    const InputLoad pre0 = unit_load(w < units ? w : 0);
-    const InputLoad pre1 = unit_load(w + GEMV_WAVES < units ? w + GEMV_WAVES : 0);
+    InputLoad pre[MOE_UNITS];
+    moe_batch_load(w, units, pre, unit_load);
     __builtin_amdgcn_sched_barrier(0);
 
     Chunk<K> ring[MOE_RING_D];
 #pragma unroll
     for (int u = 0; u < MOE_RING_D; ++u) load_chunk(ring[u], rs, off(u));
 
-    if (w < units) input_compute(pre0, unit_out(w));
-    if (w + GEMV_WAVES < units) input_compute(pre1, unit_out(w + GEMV_WAVES));
-    for (int u = w + 2 * GEMV_WAVES; u < units; u += GEMV_WAVES) input_compute(unit_load(u), unit_out(u));
+    moe_input_stage(w, units, pre, unit_load, unit_out);
     __syncthreads();
 
-    float acc[RT][2];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+    MfmaAcc<RT> acc;
+    mfma_acc_zero(acc);
     const bool first = g == 0;
     for (int t = 0; t < nb; t += MOE_RING_D) {
 #pragma unroll
@@ -434,17 +480,13 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
                 half2_t wq[4][4];
                 link_chunk(ring[u], first);
                 decode_chunk<K, CB_MUL1>(ring[u], wq);
-                dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+                mfma_dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
             }
             load_chunk(ring[u], rs, off(t + u + MOE_RING_D));
         }
     }
     __syncthreads();   // every wave is done with act before red overwrites it
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-        red[(w * MOE_MAX_RT + r) * 128 + 16 * jt + g] = acc[r][0];
-        red[(w * MOE_MAX_RT + r) * 128 + 16 * jt + g + 8] = acc[r][1];
-    }
+    mfma_partials<RT>(acc, red + w * MOE_MAX_RT * 128);
     __syncthreads();
 }
 
@@ -458,7 +500,8 @@ void moe_down_kernel(MoeArgs a) {
     const uint32_t c = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
-    const MoeGroup grp = moe_uniform(moe_resolve(a, blockIdx.z));
+    __shared__ uint32_t group_slot[8];
+    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot);
     if (!grp.leader) {
         // One workgroup per (invalid token, column group) writes its NaN row block.
         if (grp.nan_row >= 0 && split == 0 && tid < 128)

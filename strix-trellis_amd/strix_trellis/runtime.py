@@ -184,6 +184,12 @@ class Weights:
         abi.check(self.lib.strix_amd_gemv_shape(self.handle, C.byref(bps), C.byref(splits)))
         return bps.value, splits.value
 
+    def gemm_splits(self, rows):
+        """K splits of a GEMM call of `rows` rows (calls with equal counts share row bits)."""
+        splits = C.c_uint32()
+        abi.check(self.lib.strix_amd_gemm_splits(self.handle, C.c_uint64(rows), C.byref(splits)))
+        return splits.value
+
     # -- diagnostics -----------------------------------------------------------
     def decode(self, stream=None):
         torch = _t()
