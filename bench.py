@@ -510,10 +510,11 @@ def _traffic():
 def pmc_workload(ctx, launches, which="gemv"):
     """Fixed workload for counter passes, launched directly (no graph).
 
-    gemv: the headline plan over its rotation, then a plain 256 MiB device
-    copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters against known
-    bytes.  gemm: the M = 2048, 4096 -> 12288 K4 prefill plan.  moe: the C5
-    routed-expert plan."""
+    gemv: the headline plan over its rotation, then the read-only call-floor
+    kernel over 512 MiB (two launches, 1024 workgroups) and a plain 256 MiB
+    device copy, whose FETCH_SIZE / WRITE_SIZE calibrate the counters against
+    known bytes.  gemm: the M = 2048, 4096 -> 12288 K4 prefill plan.  moe: the
+    C5 routed-expert plan."""
     import torch
     import synth
     if which == "moe":
@@ -530,12 +531,18 @@ def pmc_workload(ctx, launches, which="gemv"):
     if which != "gemv":
         log(f"pmc workload {which}: {launches} launches (replay_matches_eager={ok})")
         return
+    from strix_trellis import runtime
+    big = torch.empty(128 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    sink = torch.empty(1024, dtype=torch.int32, device="cuda:0")
+    for _ in range(2):
+        runtime.stream_read(ctx, big, big.numel() * 4, 1024, sink)
     src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"pmc workload: {launches} headline launches (replay_matches_eager={ok}), 4 copies of {src.numel() * 4} bytes")
+    log(f"pmc workload: {launches} headline launches (replay_matches_eager={ok}), 2 reads of {big.numel() * 4} "
+        f"bytes, 4 copies of {src.numel() * 4} bytes")
 
 
 def run_section(ctx, which, steps, warmup):
