@@ -545,6 +545,75 @@ def pmc_workload(ctx, launches, which="gemv"):
         f"bytes, 4 copies of {src.numel() * 4} bytes")
 
 
+STAGE_PHASES = ("mfma_decode", "store_issue", "a_wait", "barrier")
+CLOCK_LIB = ROOT / "strix-trellis_amd" / "strix_trellis" / "_native" / "libstrix_trellis_clock.so"
+
+
+def stage_clock(ctx, cells):
+    """Per-stage phase cycles of the wide GEMM kernel from the instrumented
+    library (build.py --stage-clock; main() points the loader at it).
+
+    Each cell (M, I, N, K) is called directly six times; the records of the
+    last call are summarised: per kind of work item (whole tile, handoff head,
+    handoff tail), the mean cycles per K stage of each loop phase, the
+    prologue and epilogue, and the shader clock (s_memtime cycles over
+    s_memrealtime at 100 MHz).  Prints one JSON line per cell."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    import synth
+    from strix_trellis import abi, runtime
+    lib = abi.load()
+    if not hasattr(lib, "strix_amd_debug_stage_clock"):
+        raise RuntimeError(f"the loaded library is not {CLOCK_LIB.name}; run strix-trellis_amd/build.py --stage-clock")
+    rec = torch.zeros(8192 * 8 * 16, dtype=torch.int64, device="cuda:0")
+    lib.strix_amd_debug_stage_clock(C.c_void_p(rec.data_ptr()))
+    kinds = {0: "whole", 1: "head", 2: "tail"}
+    for (M, I, N, K) in cells:
+        tr, suh, svh, _ = synth.layer(I, N, K, synth.BASE_SEED + 2)
+        w = runtime.Weights(ctx, tr, suh, svh, None, "mul1")
+        x = torch.from_numpy(synth.activations(M, I, synth.BASE_SEED + 102)).to("cuda:0")
+        y = torch.empty((M, N), device="cuda:0")
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        for _ in range(6):
+            rec.zero_()
+            ev[0].record()
+            runtime.gemm(w, x, y)
+            ev[1].record()
+        torch.cuda.synchronize()
+        d = rec.view(-1, 16).cpu().numpy().astype(np.float64)
+        d = d[d[:, 10] > 0]                       # waves that ran K stages
+        st = d[:, 10]
+        ghz = (d[:, 8] - d[:, 6]) / ((d[:, 9] - d[:, 7]) * 10.0)
+        rt0 = d[:, 7].min()
+        beg, end = (d[:, 7] - rt0) / 100.0, (d[:, 9] - rt0) / 100.0
+        cell = {"M": M, "I": I, "N": N, "K": K, "call_us": round(ev[0].elapsed_time(ev[1]) * 1e3, 2),
+                "workgroups": int(len(d) // 8), "clock_ghz_p10_p50_p90": [round(float(np.percentile(ghz, q)), 2)
+                                                                           for q in (10, 50, 90)],
+                "last_end_us": round(float(end.max()), 1), "items": {}}
+        low = np.arange(len(d)) % 8 < 4           # waves 0..3, one per SIMD; 4..7 share the SIMDs
+
+        def phase_mean(sel, i):
+            return round(float((d[sel, i] / st[sel]).mean()))
+
+        for kind, name in kinds.items():
+            m = d[:, 11] == kind
+            if not m.any():
+                continue
+            per = {ph: phase_mean(m, i) for i, ph in enumerate(STAGE_PHASES)}
+            per["loop"] = int(sum(per[ph] for ph in STAGE_PHASES))
+            cell["items"][name] = {
+                "workgroups": int(m.sum() // 8), "stages": round(float(st[m].mean()), 1),
+                "cycles_per_stage": per,
+                "cycles_per_stage_waves_0_3_4_7": {ph: [phase_mean(m & low, i), phase_mean(m & ~low, i)]
+                                                   for i, ph in enumerate(STAGE_PHASES)},
+                "prologue_cycles": round(float(d[m, 4].mean())), "epilogue_cycles": round(float(d[m, 5].mean())),
+                "duration_us": round(float((end - beg)[m].mean()), 1)}
+        print(json.dumps(cell), flush=True)
+        w.destroy()
+    lib.strix_amd_debug_stage_clock(None)
+
+
 def run_section(ctx, which, steps, warmup):
     """One section of the default run with the same cells and step counts."""
     import synth
@@ -582,18 +651,25 @@ def main():
                     help="run one section (for profiling); prints that section's cells only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm", "moe"), default=None)
+    ap.add_argument("--stage-clock", action="store_true",
+                    help="per-stage phase cycles of the M = 2048 GEMMs (instrumented library)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (every box here has one MI355X); --gpus {args.gpus} "
               "is not supported", file=sys.stderr)
         sys.exit(2)
 
+    if args.stage_clock:
+        os.environ["STRIX_TRELLIS_LIB"] = str(CLOCK_LIB)
     import torch
     from strix_trellis import runtime
     import synth
     ctx = runtime.Context(0)
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+    if args.stage_clock:
+        stage_clock(ctx, ((2048, 4096, 12288, 4), (2048, 5120, 5120, 4)))
+        return
     if args.pmc_workload:
         pmc_workload(ctx, {"gemv": 256, "gemm": 16, "moe": 16}[args.pmc_workload], args.pmc_workload)
         return

@@ -7,6 +7,9 @@ Python package and the tests load it.
 
     python strix-trellis_amd/build.py            # full rebuild
     python strix-trellis_amd/build.py --changed  # only stale objects
+    python strix-trellis_amd/build.py --stage-clock
+        # instrumented copy, libstrix_trellis_clock.so: the wide GEMM kernel
+        # records per-wave phase cycles (bench.py --stage-clock reads them)
 """
 import argparse
 import concurrent.futures as cf
@@ -20,6 +23,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 OUT = PKG / "strix_trellis" / "_native" / "libstrix_trellis.so"
+CLOCK_OBJ = PKG / "_build_clock"
+CLOCK_OUT = PKG / "strix_trellis" / "_native" / "libstrix_trellis_clock.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
@@ -41,14 +46,14 @@ def _headers_mtime():
     return max((h.stat().st_mtime for h in hs), default=0.0)
 
 
-def _compile(src, changed_only, hdr_mtime):
-    obj = OBJ / (src.name + ".o")
+def _compile(src, changed_only, hdr_mtime, obj_dir=OBJ, defines=()):
+    obj = obj_dir / (src.name + ".o")
     if changed_only and obj.exists() and obj.stat().st_mtime >= max(src.stat().st_mtime, hdr_mtime):
         return obj, None
     if src.suffix == ".hip":
-        cmd = [HIPCC, *COMMON, *DEVICE, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *defines, *DEVICE, "-c", str(src), "-o", str(obj)]
     else:
-        cmd = [HIPCC, *COMMON, *HOST, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *defines, *HOST, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
@@ -57,35 +62,40 @@ def _compile(src, changed_only, hdr_mtime):
     return obj, None
 
 
-def build(changed_only=False, jobs=None):
-    OBJ.mkdir(parents=True, exist_ok=True)
-    OUT.parent.mkdir(parents=True, exist_ok=True)
+def build(changed_only=False, jobs=None, stage_clock=False):
+    """Compile and link the library; with stage_clock, the instrumented copy
+    (STX_STAGE_CLOCK=1) into its own object folder and file."""
+    obj_dir, out = (CLOCK_OBJ, CLOCK_OUT) if stage_clock else (OBJ, OUT)
+    defines = ("-DSTX_STAGE_CLOCK=1",) if stage_clock else ()
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    out.parent.mkdir(parents=True, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 4)
     hdr = _headers_mtime()
     srcs = _sources()
     with cf.ThreadPoolExecutor(jobs) as ex:
-        results = list(ex.map(lambda s: _compile(s, changed_only, hdr), srcs))
+        results = list(ex.map(lambda s: _compile(s, changed_only, hdr, obj_dir, defines), srcs))
     errors = [e for _, e in results if e]
     if errors:
         raise RuntimeError("\n\n".join(errors))
     objs = [str(o) for o, _ in results]
-    tmp = OUT.with_suffix(".so.tmp")
+    tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", str(tmp),
            f"-Wl,-rpath,{ROCM / 'lib'}", "-Wl,--no-undefined"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--changed", action="store_true", help="rebuild only stale objects")
     ap.add_argument("-j", "--jobs", type=int, default=None)
+    ap.add_argument("--stage-clock", action="store_true", help="build the phase-clock instrumented copy")
     args = ap.parse_args()
     try:
-        print(build(args.changed, args.jobs))
+        print(build(args.changed, args.jobs, args.stage_clock))
     except RuntimeError as exc:
         print(exc, file=sys.stderr)
         sys.exit(1)

@@ -70,6 +70,16 @@ static uint32_t gemm_bm(uint64_t rows, uint32_t groups) {
     return wg256 >= 256 ? 256 : 128;
 }
 
+#if STX_STAGE_CLOCK
+// Instrumented build only (build.py --stage-clock): where the wide kernel
+// writes its per-wave phase cycle records; null writes none.
+static unsigned long long* g_stage_clock = nullptr;
+extern "C" int strix_amd_debug_stage_clock(void* records) {
+    g_stage_clock = static_cast<unsigned long long*>(records);
+    return 0;
+}
+#endif
+
 hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream_t stream) {
     if (uint64_t(w.input / 16) * (w.output / 16) * 32u * w.bits >= (uint64_t(1) << 31)) return hipErrorInvalidValue;
     const uint64_t pass = gemm_pass_rows(w);
@@ -113,6 +123,9 @@ hipError_t launch_gemm(const DeviceWeights& w, const LinearCall& call, hipStream
         l.args.poll_limit = call.handoff_poll_limit;
         l.args.splits = wide ? wide_splits(m, w) : narrow_splits(w);
         l.args.planes = reinterpret_cast<float*>(hbase);   // a split pass has no handoff
+#if STX_STAGE_CLOCK
+        l.args.clock = g_stage_clock;
+#endif
         l.codebook = w.codebook;
         l.bm = gemm_bm(m, w.output / 128);
         l.stream = stream;

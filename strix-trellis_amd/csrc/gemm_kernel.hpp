@@ -56,6 +56,11 @@ struct GemmArgs {
     // +0 before the output stage.
     uint32_t splits;
     float* planes;
+#if STX_STAGE_CLOCK
+    // Instrumented build only: per-wave phase cycle records of the wide
+    // kernel, [workgroup][8 waves][16] (null: none written).
+    unsigned long long* clock;
+#endif
 };
 
 // Byte offset of the A fragment (row block rb, 32-channel block kb) of lane l.

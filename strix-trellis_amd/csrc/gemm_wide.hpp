@@ -79,6 +79,65 @@ enum : int { kItemFull = 0, kItemHead = 1, kItemTail = 2 };
 // launch.
 constexpr uint32_t kHandoffForceRecompute = 0xFFFFFFFFu;   // poll_limit: always take over
 
+// Phase clock of one wave (s_memtime, shader clock cycles), compiled in only
+// by the instrumented build (STX_STAGE_CLOCK=1, build.py --stage-clock); in
+// the product build every member is empty.  Per K stage the loop is cut into
+//   0: MFMAs of stage st with the interleaved decode of stage st + 1,
+//   1: the decoded B fragments to LDS and the next chunk loads issued,
+//   2: the wait for A stage st + 1 (vmcnt),
+//   3: the stage barrier;
+// scheduling barriers pin each mark, so the instrumented loop keeps these
+// phases in this order.  A record is 16 words per wave:
+//   [phase 0..3 sums][prologue][epilogue][t0][realtime0][t1][realtime1]
+//   [stages][kind][tile][first stage][split][0]
+// (s_memrealtime counts at 100 MHz).
+struct StageClock {
+#if STX_STAGE_CLOCK
+    uint64_t phase[4] = {0, 0, 0, 0};
+    uint64_t t0 = 0, rt0 = 0, loop0 = 0, loop1 = 0, mark = 0;
+    uint32_t stages = 0;
+    __device__ __forceinline__ static uint64_t now() {
+        __builtin_amdgcn_sched_barrier(0);
+        const uint64_t t = __builtin_amdgcn_s_memtime();
+        __builtin_amdgcn_sched_barrier(0);
+        return t;
+    }
+    __device__ __forceinline__ void begin() {
+        t0 = __builtin_amdgcn_s_memtime();
+        rt0 = __builtin_amdgcn_s_memrealtime();
+    }
+    __device__ __forceinline__ void loop_begin() { loop0 = now(); }
+    __device__ __forceinline__ void stage_begin() { mark = now(); }
+    template <int I>
+    __device__ __forceinline__ void phase_end() {
+        const uint64_t t = now();
+        phase[I] += t - mark;
+        mark = t;
+    }
+    __device__ __forceinline__ void stage_end() { ++stages; }
+    __device__ __forceinline__ void loop_end() { loop1 = now(); }
+    __device__ __forceinline__ void record(const GemmArgs& a, int kind, uint32_t tile, uint32_t s0) const {
+        const uint64_t t1 = now(), rt1 = __builtin_amdgcn_s_memrealtime();
+        if (!a.clock || (threadIdx.x & 63) != 0) return;
+        const uint64_t wg = uint64_t(blockIdx.y) * gridDim.x + blockIdx.x;
+        auto* r = (__attribute__((address_space(1))) unsigned long long*)(a.clock + (wg * 8 + (threadIdx.x >> 6)) * 16);
+        const uint64_t v[16] = {phase[0], phase[1], phase[2], phase[3], loop0 - t0, t1 - loop1, t0, rt0,
+                                t1, rt1, stages, uint64_t(kind), tile, s0, blockIdx.y, 0};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r[i] = v[i];
+    }
+#else
+    __device__ __forceinline__ void begin() {}
+    __device__ __forceinline__ void loop_begin() {}
+    __device__ __forceinline__ void stage_begin() {}
+    template <int I>
+    __device__ __forceinline__ void phase_end() {}
+    __device__ __forceinline__ void stage_end() {}
+    __device__ __forceinline__ void loop_end() {}
+    __device__ __forceinline__ void record(const GemmArgs&, int, uint32_t, uint32_t) const {}
+#endif
+};
+
 // Each wave owns the 128 channels of one output H128 group and TM 32-row
 // blocks: BN = 256 as 4 (M) x 2 (N) waves of 64 rows, all eight decode;
 // BN = 128 as 8 (M) x 1 (N) waves of 32 rows, the stage's 8 tiles x 4 blocks
@@ -100,6 +159,8 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     const int wm = w / WN, wn = w % WN;
     const int jt8 = lane >> 3, g = lane & 7;
     const uint32_t I = a.I, N = a.N, stages = I / 64, half = stages / 2;
+    StageClock clk;
+    clk.begin();
 
     constexpr uint32_t tile_bytes = 32u * K;
     const uint32_t row_bytes = (N >> 4) * tile_bytes;
@@ -266,11 +327,13 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     load_stage(ring[0], s0 + D);
     __builtin_amdgcn_sched_barrier(0);
     stage_barrier(std::integral_constant<int, 4 + kChunkOps>{});   // A stage s0 landed
+    clk.loop_begin();
 
     for (uint32_t st0 = s0; st0 < s_end; st0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const uint32_t st = st0 + d;
+            clk.stage_begin();
             __builtin_amdgcn_sched_barrier(0);
             dma_a(st + 2);
             __builtin_amdgcn_sched_barrier(0);
@@ -310,18 +373,29 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             }
             // Decoded stage st + 1 -> the other B buffer (past the end: zeros
             // of out-of-range loads into an unused buffer).
+            clk.phase_end<0>();
             if (decoder) store_bfrag(wq, (st + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
             load_stage(ring[slot], st + 1 + D);
             __builtin_amdgcn_sched_barrier(0);
+            clk.phase_end<1>();
             // A stage st + 1 (issued one stage ago) has landed once at most the
             // last stage's chunk loads, this stage's 4 DMAs and chunk loads remain.
+#if STX_STAGE_CLOCK
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(4 + 2 * kChunkOps) : "memory");
+            clk.phase_end<2>();
+            asm volatile("s_barrier" ::: "memory");
+            clk.phase_end<3>();
+            clk.stage_end();
+#else
             stage_barrier(std::integral_constant<int, 4 + 2 * kChunkOps>{});
+#endif
         }
     }
     // The last stages issued A DMAs past the end (dummy rows into A buffers):
     // they land before LDS is reused as the epilogue tile or by the next item.
     stage_barrier(std::integral_constant<int, 0>{});
+    clk.loop_end();
 
     // Lane l holds rows 32 (TM wm + im) + l % 32 of the tile and, per MFMA
     // tile jn and accumulator r, channel 32 jn + 8 (r / 4) + 4 (l / 32) + r % 4
@@ -347,6 +421,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
                 for (int r4 = 0; r4 < 4; ++r4)
                     __builtin_amdgcn_raw_buffer_store_b128(acc4(jn, im, r4), prsrc, out_off + (32 * jn + 8 * r4) * 4,
                                                            32 * im * N * 4, 0);
+        clk.record(a, kind, t, s0);
         return;
     }
 
@@ -367,6 +442,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
                 __hip_atomic_store(a.flags + hslot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // abandoned
         }
+        clk.record(a, kind, t, s0);
         return;
     }
 
@@ -492,6 +568,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         h128(second, v);
         emit_any(second, v);
     }
+    clk.record(a, kind, t, s0);
 }
 
 template <int K>

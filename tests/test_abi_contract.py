@@ -36,6 +36,18 @@ def test_library_exports_every_declared_function():
             assert hasattr(lib, name)
 
 
+def test_stage_clock_only_in_the_instrumented_build():
+    # The phase-clock hook is compiled only with STX_STAGE_CLOCK=1 (build.py --stage-clock).
+    out = subprocess.run(["nm", "-D", "--defined-only", str(abi.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    assert "strix_amd_debug_stage_clock" not in out
+    clock = abi.LIB_PATH.with_name("libstrix_trellis_clock.so")
+    if not clock.exists():
+        pytest.skip("instrumented library not built")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(clock)], capture_output=True, text=True, check=True).stdout
+    assert " T strix_amd_debug_stage_clock" in out
+
+
 STRUCTS = {
     "strix_exl3_metadata_v1": abi.Metadata, "strix_exl3_transport_desc": abi.TransportDesc,
     "strix_host_region": abi.HostRegion, "strix_exl3_parts_desc": abi.PartsDesc, "strix_stream": abi.Stream,
