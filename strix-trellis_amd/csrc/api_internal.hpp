@@ -15,6 +15,7 @@
 #include "backend.hpp"
 
 #include <cstring>
+#include <utility>
 #include <vector>
 
 struct strix_context_impl {
@@ -37,6 +38,16 @@ struct strix_weights_impl {
     // weights.  Graphs captured from a plan may replay after the plan is
     // destroyed, so the arrays live until the weights are destroyed.
     std::vector<void*> counter_arrays;
+    // Blocks of counter_arrays whose plans were destroyed: a later plan that
+    // needs a block of the same size re-initialises and takes one, so the
+    // state held stays bounded by the plans alive at one time.
+    std::vector<std::pair<void*, uint64_t>> idle_states;
+};
+
+// A single-launch state block held by a plan (base of a counter_arrays block).
+struct FusedBlock {
+    void* base = nullptr;
+    uint64_t bytes = 0;
 };
 
 struct strix_linear_plan_impl {
@@ -46,6 +57,7 @@ struct strix_linear_plan_impl {
     hipStream_t stream{};
     bool gemm = false;
     stx::FusedState fused{};    // single-launch GEMV state (null when one split suffices)
+    FusedBlock block{};
     uint32_t launches = 0;
 };
 
@@ -139,8 +151,12 @@ stx::LinearCall to_call(const strix_matmul_desc& d, uint64_t rows, void* workspa
 // status and epochs 0, every plane word GEMV_PLANE_EMPTY.
 hipError_t init_fused_state(void* base, uint64_t bytes, uint64_t planes_offset, hipStream_t hs);
 // Initialised single-launch GEMV state for `rows` rows on `w` (none when one
-// split suffices), owned by the weights; the stream is synchronised.
-strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, stx::FusedState& out);
+// split suffices), owned by the weights: an idle block of the same size if
+// there is one, else a new one; the stream is synchronised.
+strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, stx::FusedState& out,
+                              FusedBlock& block);
+// A destroyed plan's block becomes idle (it stays allocated with the weights).
+void release_fused_state(strix_weights w, FusedBlock& block);
 // Sticky status word of a single-launch state: read (synchronising `hs`) and
 // optionally cleared.
 strix_status read_fused_status(const stx::FusedState& st, hipStream_t hs, uint32_t* flags, uint32_t clear);

@@ -23,15 +23,26 @@ hipError_t init_fused_state(void* base, uint64_t bytes, uint64_t planes_offset, 
     return stx::launch_fill_u32(words + planes_offset / 4, stx::GEMV_PLANE_EMPTY, (bytes - planes_offset) / 4, hs);
 }
 
-strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, stx::FusedState& out) {
+strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, stx::FusedState& out,
+                              FusedBlock& block) {
     out = {};
+    block = {};
     const uint64_t bytes = stx::fused_state_bytes(w->dev, rows, 1);
     if (!bytes) return STRIX_SUCCESS;
     void* state = nullptr;
-    hipError_t e = hipMalloc(&state, bytes);
+    bool reused = false;
+    for (auto it = w->idle_states.begin(); it != w->idle_states.end(); ++it) {
+        if (it->second == bytes) {
+            state = it->first;
+            w->idle_states.erase(it);
+            reused = true;
+            break;
+        }
+    }
+    hipError_t e = reused ? hipSuccess : hipMalloc(&state, bytes);
     if (e == hipSuccess) e = init_fused_state(state, bytes, stx::fused_planes_offset(w->dev, 1), hs);
     if (e == hipSuccess) e = hipStreamSynchronize(hs);
-    if (e == hipSuccess) {
+    if (e == hipSuccess && !reused) {
         try {
             w->counter_arrays.push_back(state);   // released with the weights
         } catch (...) {
@@ -39,11 +50,26 @@ strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, st
         }
     }
     if (e != hipSuccess) {
-        if (state) (void)hipFree(state);
+        FusedBlock back{state, bytes};
+        if (reused)
+            release_fused_state(w, back);   // still owned by the weights; initialised again on reuse
+        else if (state)
+            (void)hipFree(state);
         return status_of(e);
     }
+    block = {state, bytes};
     out = stx::fused_state_at(state, w->dev, rows, 1);
     return STRIX_SUCCESS;
+}
+
+void release_fused_state(strix_weights w, FusedBlock& block) {
+    if (!block.base) return;
+    try {
+        w->idle_states.emplace_back(block.base, block.bytes);
+    } catch (...) {
+        // not reusable then; it is still freed with the weights
+    }
+    block = {};
 }
 
 strix_status read_fused_status(const stx::FusedState& st, hipStream_t hs, uint32_t* flags, uint32_t clear) {
@@ -166,7 +192,7 @@ strix_status strix_linear_plan_create(strix_context c, const strix_matmul_desc* 
     plan->gemm = gemm;
     plan->call = to_call(*d, e.rows, d->workspace);
     if (!gemm && e.rows) {
-        const strix_status s = make_fused_state(w, e.rows, hs, plan->fused);
+        const strix_status s = make_fused_state(w, e.rows, hs, plan->fused, plan->block);
         if (s != STRIX_SUCCESS) {
             delete plan;
             return s;
@@ -191,6 +217,7 @@ strix_status strix_linear_plan_submit(strix_linear_plan p) {
 
 strix_status strix_linear_plan_destroy(strix_linear_plan p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
+    release_fused_state(p->weights, p->block);
     --p->weights->plans;
     delete p;
     return STRIX_SUCCESS;

@@ -32,6 +32,7 @@ struct TpMember {
     strix_weights weights = nullptr;
     stx::LinearCall call{};
     stx::FusedState fused{};
+    FusedBlock block{};
 };
 }  // namespace
 
@@ -113,7 +114,7 @@ strix_status member_ok(strix_context c, strix_weights w, const strix_tensor_desc
 // Single-launch state for every member (freed with its weights), zeroed.
 strix_status arm(std::vector<TpMember>& members, hipStream_t hs) {
     for (TpMember& m : members) {
-        const strix_status s = make_fused_state(m.weights, m.call.rows, hs, m.fused);
+        const strix_status s = make_fused_state(m.weights, m.call.rows, hs, m.fused, m.block);
         if (s != STRIX_SUCCESS) return s;
     }
     return STRIX_SUCCESS;
@@ -123,6 +124,7 @@ template <class Plan>
 strix_status finish_create(Plan* p, strix_context c, hipStream_t hs) {
     strix_status s = arm(p->members, hs);
     if (s != STRIX_SUCCESS) {
+        for (TpMember& m : p->members) release_fused_state(m.weights, m.block);
         if (p->scratch) (void)hipFree(p->scratch);
         delete p;
         return s;
@@ -234,7 +236,10 @@ strix_status plan_destroy(strix_tp_dense_plan_impl* p) {
         const hipError_t e = hipFree(p->scratch);
         if (e != hipSuccess) return status_of(e);
     }
-    for (TpMember& m : p->members) --m.weights->plans;
+    for (TpMember& m : p->members) {
+        release_fused_state(m.weights, m.block);
+        --m.weights->plans;
+    }
     delete p;
     return STRIX_SUCCESS;
 }

@@ -421,6 +421,33 @@ static void direct_calls(strix_context c, hipStream_t hs) {
     fake::reset_failures();
     STATUS(strix_linear_plan_create(c, &m, &st, 7, &bad), STRIX_ERROR_INVALID_ARGUMENT);
 
+    // Create/destroy cycles: a destroyed plan's planes become idle and the
+    // next plan of the same size takes them, initialised again (two fills)
+    // with no allocation, so the state held stays bounded.
+    m = matmul(d, 4, 2);
+    const size_t live2 = fake::live.size();
+    for (int cycle = 0; cycle < 4; ++cycle) {
+        fake::launches.clear();
+        const fake::Counters c0 = fake::n;
+        strix_linear_plan tp = nullptr;
+        STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &tp), STRIX_SUCCESS);
+        CHECK(fake::n.mallocs == c0.mallocs + (cycle == 0 ? 1 : 0));   // gp still holds the first block
+        CHECK(fake::live.size() == live2 + 1);
+        CHECK(fake::launches.size() == 2 && fake::launches[0].name == "fill" && fake::launches[1].name == "fill");
+        STATUS(strix_linear_plan_destroy(tp), STRIX_SUCCESS);
+        CHECK(fake::live.size() == live2 + 1);
+    }
+    // A failed re-initialisation keeps the idle block for the next plan.
+    fake::launch_fail_at = 0;
+    STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &bad), STRIX_ERROR_BACKEND);
+    fake::reset_failures();
+    CHECK(bad == nullptr && fake::live.size() == live2 + 1);
+    const fake::Counters c1 = fake::n;
+    strix_linear_plan again = nullptr;
+    STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &again), STRIX_SUCCESS);
+    CHECK(fake::n.mallocs == c1.mallocs && fake::live.size() == live2 + 1);
+    STATUS(strix_linear_plan_destroy(again), STRIX_SUCCESS);
+
     // Weights outlive their plans; the planes go with the weights.
     STATUS(strix_weights_destroy(d.w), STRIX_ERROR_INVALID_ARGUMENT);
     STATUS(strix_linear_plan_destroy(gp), STRIX_SUCCESS);

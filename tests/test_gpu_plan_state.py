@@ -11,7 +11,9 @@ every kernel still exits normally) and check that
     two-launch strix_gemv, although the given-up launch's partials landed in
     the planes after its finisher left (their tag is stale);
   * many submissions in a row, with inputs rewritten between them, each carry
-    the bits of strix_gemv (the epoch advances every launch).
+    the bits of strix_gemv (the epoch advances every launch);
+  * a plan created after another was destroyed takes over its planes,
+    initialised again.
 
 Also the call-floor kernel (strix_amd_stream_read): every workgroup's XOR of
 its slice of the source.
@@ -144,6 +146,44 @@ def test_grouped_plan_give_up_then_exact(ctx):
         plan.destroy()
         for w in ws:
             w.destroy()
+
+
+def test_plan_state_reused_after_destroy(ctx):
+    # A destroyed plan's planes go idle and the next plan of the same rows on
+    # the same weights takes them, initialised again: the new plan neither
+    # inherits the old one's sticky give-up nor folds its stale partials.
+    I, N, K, R = 4096, 4096, 4, 2
+    print(f"plan state reuse {I}x{N} K{K} R{R}", flush=True)
+    tr, suh, svh, _ = synth.layer(I, N, K, synth.BASE_SEED + 90)
+    w = runtime.Weights(ctx, tr, suh, svh, None, "mul1")
+    x = torch.from_numpy(synth.activations(R, I, synth.BASE_SEED + 91)).to(DEV)
+    y = torch.empty((R, N), device=DEV)
+    ref = torch.empty((R, N), device=DEV)
+    runtime.gemv(w, x, ref)
+    first = runtime.LinearPlan(w, x, y)
+    second = None
+    try:
+        ctx.set_gemv_poll_limit(0)
+        first.submit()
+        torch.cuda.synchronize()
+        assert first.status() == abi.GEMV_GAVE_UP
+        ctx.set_gemv_poll_limit(abi.GEMV_POLL_DEFAULT)
+        first.destroy()
+        first = None
+        second = runtime.LinearPlan(w, x, y)
+        assert second.status() == 0
+        for rep in range(4):
+            y.fill_(0.0)
+            second.submit()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(_bits(y), _bits(ref), err_msg=f"submission {rep} of the second plan")
+        assert second.status() == 0
+    finally:
+        ctx.set_gemv_poll_limit(abi.GEMV_POLL_DEFAULT)
+        for plan in (first, second):
+            if plan is not None:
+                plan.destroy()
+        w.destroy()
 
 
 @pytest.mark.parametrize("nbytes,wgs", [(8 << 20, 512), (1 << 20, 64), (4096, 1)])
