@@ -76,7 +76,13 @@ enum : int { kItemFull = 0, kItemHead = 1, kItemTail = 2 };
 // (bounded; its head was dispatched before it, so the wait ends); when the
 // head is late it takes the tile over from K = 0 instead, and whichever of the
 // two comes second puts the flag back to 0, so it is 0 at the end of every
-// launch.
+// launch.  The head publishes with an agent-scope release CAS after its
+// partial stores (and a workgroup barrier), the tail polls with agent-scope
+// acquire loads before a barrier that orders its waves' partial loads: the
+// partials are ordered before the flag in the language's memory model, not
+// only by the hardware's write-through stores and wait counts.  (Measured:
+// the release's L2 write-back and the acquire's invalidate cost no
+// measurable time at M = 2048.)
 constexpr uint32_t kHandoffForceRecompute = 0xFFFFFFFFu;   // poll_limit: always take over
 
 // Phase clock of one wave (s_memtime, shader clock cycles), compiled in only
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             int take = 0;
             if (a.poll_limit != kHandoffForceRecompute) {
                 for (uint32_t spin = 0;; ++spin) {
-                    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u) {
+                    if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 1u) {
                         take = 1;
                         break;
                     }
@@ -438,7 +444,7 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
         __syncthreads();
         if (tid == 0) {
             uint32_t expected = 0;
-            if (!__hip_atomic_compare_exchange_strong(a.flags + hslot, &expected, 1u, __ATOMIC_RELAXED,
+            if (!__hip_atomic_compare_exchange_strong(a.flags + hslot, &expected, 1u, __ATOMIC_RELEASE,
                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
                 __hip_atomic_store(a.flags + hslot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // abandoned
         }
