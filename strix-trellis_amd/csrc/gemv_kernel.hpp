@@ -15,10 +15,9 @@
 //     ring are issued before it so their latency overlaps it;
 //   * main loop: wave w takes input blocks w, w+4, ...; per block every lane
 //     loads its K-word chunk (K*256 contiguous bytes per wave), decodes 32
-//     weights in VGPRs, moves them into matrix-core operand order with eight
-//     v_permlane32_swap and multiplies them with the block's activations (read
-//     from LDS by broadcast) in 8 or 16 v_mfma_f32_4x4x4_16b_f16, whatever the
-//     row count up to four or eight;
+//     weights in VGPRs and multiplies them, as the B operand of 8 or 16
+//     v_mfma_f32_4x4x4_16b_f16 (row counts up to four or eight), with the
+//     block's activations read from LDS;
 //   * the four waves' partial sums meet in LDS and are added in wave order;
 //   * S == 1: the workgroup applies the output stage itself.  Otherwise it
 //     writes its [rows][128] partial plane; the finishing step (a second
@@ -274,23 +273,22 @@ __device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeig
 // Matrix-core dot: v_mfma_f32_4x4x4_16b_f16, sixteen 4x4x4 products per
 // instruction.  Operand layout, checked on the device: block b uses lanes
 // 4b..4b+3; A[b][i][k] sits in lane 4b+i, B[b][k][j] in lane 4b+j (halves
-// k = 0..3), D[b][i][j] in lane 4b+j, element i.  Here A is 64 weight
-// columns (A row = lane), B the activations of four rows, D their products.
-//
-// A decoded chunk (lane 8t+g holds columns g and g+8 of tile t, input rows
-// 0..15 of the block: wq[V][khalf + 2 sel], sel selecting column g + 8 sel)
-// becomes the A operands by one v_permlane32_swap per register pair
-// (sel 0, sel 1): the first register then holds tiles 0..3 and the second
-// tiles 4..7 (half h = 0, 1), with lane bit 5 selecting the column.  So A row
-// p of half h is output column
-//   chan(p, h) = 16 ((p >> 3) & 3) + 8 (p >> 5) + (p & 7) + 64 h,
-// and K step q (block rows 4q..4q+3) of half h is wq[2 (q & 1)][q / 2 + 2 h]
-// followed by wq[2 (q & 1) + 1][q / 2 + 2 h].  B (step q, row quad rh): lane l
-// reads activation row 4 rh + l % 4, clamped to RT - 1 (a D column of a row
-// past RT is never read), block rows 4q..4q+3.
+// k = 0..3), D[b][i][j] in lane 4b+j, element i.  Here A holds the
+// activations of four rows and B the decoded weights, so every lane feeds
+// its own decoded columns as B with no data movement across lanes:
+//   * lane 8t+g holds columns g and g+8 (half h = 0, 1) of tile t, input
+//     rows 0..15 of the block (wq[V][khalf + 2h]); K step q (block rows
+//     4q..4q+3) of half h is wq[2 (q & 1)][q / 2 + 2 h] followed by
+//     wq[2 (q & 1) + 1][q / 2 + 2 h];
+//   * A (step q, row quad rh): lane l reads activation row 4 rh + l % 4,
+//     clamped to RT - 1 (rows past RT are never read back), block rows
+//     4q..4q+3, the same for every block b;
+//   * D[h][rh] of lane l, element i, is row 4 rh + i of output column
+//     16 (l >> 3) + (l & 7) + 8 h of the 128-column group.
 // Per output: +0, then blocks in ascending order, within a block K steps
-// q = 0..3 (four products each, in the hardware's order).  D columns are
-// independent, so a row's bits do not depend on the other rows.
+// q = 0..3 (four products each, in the hardware's order).  A row's products
+// are the D elements of its own A row, so its bits do not depend on the
+// other rows.
 // ---------------------------------------------------------------------------
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float gemv_f4_t __attribute__((ext_vector_type(4)));
@@ -311,77 +309,45 @@ __device__ __forceinline__ void mfma_acc_zero(MfmaAcc<RT>& acc) {
 
 __device__ __forceinline__ half4_t join_h4(half2_t lo, half2_t hi) { return half4_t{lo.x, lo.y, hi.x, hi.y}; }
 
-// One decoded block (wq, consumed) against the activations `act` of its 16
-// input rows (act + r * act_row: activation row r).
+// One decoded block (wq) against the activations `act` of its 16 input rows
+// (act + r * act_row: activation row r).
 template <int RT>
-__device__ __forceinline__ void mfma_dot_block(half2_t (&wq)[4][4], const _Float16* act, uint32_t act_row,
+__device__ __forceinline__ void mfma_dot_block(const half2_t (&wq)[4][4], const _Float16* act, uint32_t act_row,
                                                MfmaAcc<RT>& acc) {
     constexpr int RH = MfmaAcc<RT>::RH;
     const int lane = threadIdx.x & 63;
-    half4_t xb[4][RH];
+    half4_t xa[4][RH];
 #pragma unroll
     for (int rh = 0; rh < RH; ++rh) {
         const int row = 4 * rh + (lane & 3) < RT ? 4 * rh + (lane & 3) : RT - 1;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xb[q][rh] = *reinterpret_cast<const half4_t*>(act + row * act_row + 4 * q);
+        for (int q = 0; q < 4; ++q) xa[q][rh] = *reinterpret_cast<const half4_t*>(act + row * act_row + 4 * q);
     }
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(as_u32(wq[v][kh]), as_u32(wq[v][kh + 2]), false, false);
-            wq[v][kh] = as_h2(sw[0]);
-            wq[v][kh + 2] = as_h2(sw[1]);
-        }
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const half4_t av = join_h4(wq[2 * (q & 1)][q / 2 + 2 * h], wq[2 * (q & 1) + 1][q / 2 + 2 * h]);
+            const half4_t wb = join_h4(wq[2 * (q & 1)][q / 2 + 2 * h], wq[2 * (q & 1) + 1][q / 2 + 2 * h]);
 #pragma unroll
             for (int rh = 0; rh < RH; ++rh)
-                acc.d[h][rh] = __builtin_amdgcn_mfma_f32_4x4x4f16(av, xb[q][rh], acc.d[h][rh], 0, 0, 0);
+                acc.d[h][rh] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[q][rh], wb, acc.d[h][rh], 0, 0, 0);
         }
 }
 
-// The wave's sums to `red` ([RT][128] F32, row-major): lane 4b+j holds row
-// 4 rh + j, columns chan(4b + i, h) for i = 0..3, four consecutive columns.
+// The wave's sums to `red` ([RT][128] F32, row-major): lane l holds rows
+// 4 rh + i (element i) of columns 16 (l >> 3) + (l & 7) + 8 h.
 template <int RT>
 __device__ __forceinline__ void mfma_partials(const MfmaAcc<RT>& acc, float* red) {
-    const int lane = threadIdx.x & 63, b = lane >> 2;
-    const int ch0 = 4 * (b & 1) + 16 * ((b >> 1) & 3) + 8 * (b >> 3);
+    const int lane = threadIdx.x & 63;
+    const int col = 16 * (lane >> 3) + (lane & 7);
 #pragma unroll
-    for (int rh = 0; rh < MfmaAcc<RT>::RH; ++rh) {
-        const int row = 4 * rh + (lane & 3);
-        if (row < RT) {
+    for (int rh = 0; rh < MfmaAcc<RT>::RH; ++rh)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) *reinterpret_cast<gemv_f4_t*>(red + row * 128 + ch0 + 64 * h) = acc.d[h][rh];
-        }
-    }
-}
-
-// Dot of one decoded chunk (32 weights: columns g and g+8, rows 0..15 of one
-// input block) with the block's FP16 activations of every row.
-template <int RT>
-__device__ __forceinline__ void dot_block(const half2_t (&wq)[4][4], const _Float16* act, uint32_t act_row,
-                                          float (&acc)[RT][2]) {
+        for (int i = 0; i < 4; ++i)
+            if (4 * rh + i < RT) {
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(act + r * act_row);
-        const u32x4 lo = p[0], hi = p[1];
-        const half2_t xp[8] = {as_h2(lo.x), as_h2(lo.y), as_h2(lo.z), as_h2(lo.w),
-                               as_h2(hi.x), as_h2(hi.y), as_h2(hi.z), as_h2(hi.w)};
-        float a0 = acc[r][0], a1 = acc[r][1];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            a0 = __builtin_amdgcn_fdot2(wq[v][0], xp[v], a0, false);
-            a0 = __builtin_amdgcn_fdot2(wq[v][1], xp[v + 4], a0, false);
-            a1 = __builtin_amdgcn_fdot2(wq[v][2], xp[v], a1, false);
-            a1 = __builtin_amdgcn_fdot2(wq[v][3], xp[v + 4], a1, false);
-        }
-        acc[r][0] = a0;
-        acc[r][1] = a1;
-    }
+                for (int h = 0; h < 2; ++h) red[(4 * rh + i) * 128 + col + 8 * h] = acc.d[h][rh][i];
+            }
 }
 
 // Register budget: five waves per SIMD (<= 96 VGPRs), measured faster than
