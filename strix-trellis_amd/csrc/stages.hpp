@@ -35,8 +35,9 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
 }
 
 // v of lane l ^ S, without the LDS crossbar: DPP quad permutes for strides 1
-// and 2, row shifts for 4, a row rotate for 8, and the gfx950 permlane swaps
-// (odd/even 16-lane rows, upper/lower 32-lane halves) for 16 and 32.
+// and 2, two bank-masked row shifts for 4, a row rotate for 8, and the gfx950
+// permlane swaps (odd/even 16-lane rows, upper/lower 32-lane halves) for 16
+// and 32.
 template <int S>
 __device__ __forceinline__ float xor_lane(float v) {
     const int lane = threadIdx.x & 63;
@@ -46,9 +47,10 @@ __device__ __forceinline__ float xor_lane(float v) {
     } else if constexpr (S == 2) {
         return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
     } else if constexpr (S == 4) {
-        const int up = __builtin_amdgcn_mov_dpp(iv, 0x104, 0xf, 0xf, false);     // row_shl:4 -> lane + 4
-        const int down = __builtin_amdgcn_mov_dpp(iv, 0x114, 0xf, 0xf, false);   // row_shr:4 -> lane - 4
-        return __builtin_bit_cast(float, (lane & 4) ? down : up);
+        // Banks 0 and 2 of each row (lanes 0-3, 8-11) take lane + 4 (row_shl:4),
+        // banks 1 and 3 take lane - 4 (row_shr:4) over that result.
+        const int up = __builtin_amdgcn_update_dpp(iv, iv, 0x104, 0xf, 0x5, false);
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(up, iv, 0x114, 0xf, 0xA, false));
     } else if constexpr (S == 8) {
         return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x128, 0xf, 0xf, false));  // row_ror:8
     } else if constexpr (S == 16) {
@@ -61,12 +63,50 @@ __device__ __forceinline__ float xor_lane(float v) {
     }
 }
 
+// +1 on lanes with bit S clear, -1 where it is set.
+template <int S>
+__device__ __forceinline__ float lane_sign() {
+    return (threadIdx.x & S) ? -1.0f : 1.0f;
+}
+
+// One butterfly level at DPP stride S (1, 2, 4, 8) on a lane's value: the
+// lower lane keeps own + partner, the upper one partner - own.  Both are
+// fma(sign, own, partner): sign * own is exact (a sign flip), so the fma
+// rounds once, to the same bits as the add or subtract, signed zeros
+// included (a NaN operand gives a NaN either way).
+template <int S>
+__device__ __forceinline__ float bfly_lane(float v, float sign) {
+    return __builtin_fmaf(sign, v, xor_lane<S>(v));
+}
+
+// The level at stride 16 or 32 on the lane's two values at once: one swap
+// puts each lane's value beside its partner's (own and partner of v0 on the
+// lower lanes, of v1 on the upper ones), one add and one subtract form both
+// results in the operand order above, and a second swap returns them to
+// their lanes.
+template <int S>
+__device__ __forceinline__ void bfly_pair(float& v0, float& v1) {
+    static_assert(S == 16 || S == 32, "swap stride");
+    const uint32_t a = __builtin_bit_cast(uint32_t, v0), b = __builtin_bit_cast(uint32_t, v1);
+    const auto s1 = S == 16 ? __builtin_amdgcn_permlane16_swap(a, b, false, false)
+                            : __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    const float x = __builtin_bit_cast(float, uint32_t(s1[0])), y = __builtin_bit_cast(float, uint32_t(s1[1]));
+    const uint32_t lo = __builtin_bit_cast(uint32_t, x + y), hi = __builtin_bit_cast(uint32_t, x - y);
+    const auto s2 = S == 16 ? __builtin_amdgcn_permlane16_swap(lo, hi, false, false)
+                            : __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+    v0 = __builtin_bit_cast(float, uint32_t(s2[0]));
+    v1 = __builtin_bit_cast(float, uint32_t(s2[1]));
+}
+
 template <int S>
 __device__ __forceinline__ void butterfly(float& v0, float& v1) {
-    const bool upper = (threadIdx.x & S) != 0;
-    const float p0 = xor_lane<S>(v0), p1 = xor_lane<S>(v1);
-    v0 = upper ? p0 - v0 : v0 + p0;
-    v1 = upper ? p1 - v1 : v1 + p1;
+    if constexpr (S >= 16) {
+        bfly_pair<S>(v0, v1);
+    } else {
+        const float sign = lane_sign<S>();
+        v0 = bfly_lane<S>(v0, sign);
+        v1 = bfly_lane<S>(v1, sign);
+    }
 }
 
 __device__ __forceinline__ void h32_wave(float& v0, float& v1) {
@@ -89,18 +129,8 @@ template <int P>
 __device__ __forceinline__ void h32_wave_multi(float (&v0)[P], float (&v1)[P]) {
     auto stage = [&](auto s) {
         constexpr int S = decltype(s)::value;
-        const bool upper = (threadIdx.x & S) != 0;
-        float p0[P], p1[P];
 #pragma unroll
-        for (int i = 0; i < P; ++i) {
-            p0[i] = xor_lane<S>(v0[i]);
-            p1[i] = xor_lane<S>(v1[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-            v0[i] = upper ? p0[i] - v0[i] : v0[i] + p0[i];
-            v1[i] = upper ? p1[i] - v1[i] : v1[i] + p1[i];
-        }
+        for (int i = 0; i < P; ++i) butterfly<S>(v0[i], v1[i]);
     };
     stage(std::integral_constant<int, 1>{});
     stage(std::integral_constant<int, 2>{});
