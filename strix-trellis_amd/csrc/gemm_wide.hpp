@@ -240,15 +240,21 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
             *reinterpret_cast<volatile int*>(smem) = take;
         }
         __syncthreads();
-        if (*reinterpret_cast<volatile int*>(smem)) s0 = half;
+        // Uniform (readfirstlane): the K loop's counter then stays scalar.
+        if (__builtin_amdgcn_readfirstlane(*reinterpret_cast<volatile int*>(smem))) s0 = half;
         __syncthreads();   // every wave has read it before the prologue's DMAs reuse the word
     }
 
     // ---- B: chunk ring (stage st in slot st % D), one chunk per lane ----
     constexpr int D = 1;   // chunk ring depth; 2 would spill at 256 VGPRs
     Chunk<K> ring[D];
+    // The stage's part of the offset is a scalar operand.  Past the end, or for
+    // a wave that does not decode, the lane offset itself goes out of range:
+    // the buffer range check covers the vector and immediate offsets, not the
+    // scalar one.
     auto load_stage = [&](Chunk<K>& dst, uint32_t st) {
-        load_chunk(dst, wrsrc, (decoder && st < s_end) ? (st * 4 + dblk) * row_bytes + lane_off : 0x80000000u);
+        const bool live = decoder && st < s_end;
+        load_chunk(dst, wrsrc, lane_off + (live ? 0u : 0x80000000u), live ? (st * 4 + dblk) * row_bytes : 0u);
     };
     // Lane (tile dtile, chunk g) holds rows 0..15 of tile columns g and g+8 of
     // input block dblk: column n = 16 (dtile % 2) + g (+8) of 32-column block
@@ -274,16 +280,23 @@ __global__ __launch_bounds__(512) void gemm_wide_kernel(GemmArgs a) {
     // ---- A: wave w DMAs fragments 4w..4w+3 (fragment f = 32-row block f/4,
     // K16 step f%4) of a stage straight into LDS (buffer_load ... lds).  Three
     // A buffers: stage st is issued two stages ahead, into buffer st % 3.
+    // Lane part of the fragment offsets (row block 8 mb + w); the stage's K
+    // part is a scalar operand (always in range), and K16 step q the
+    // immediate offset q * 1 KiB, which the load adds to both the memory and
+    // the LDS address.
+    const uint32_t a_voff = uint32_t(afrag32_offset(uint32_t(mb) * 8 + w, 0, I, lane));
     auto dma_a = [&](uint32_t st) {
-        const uint32_t kb = st < s_end ? 4 * st : 0;
-        unsigned char* base = abuf + (st % 3) * WIDE_TILE_BYTES;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int f = 4 * w + q;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                arsrc, (__attribute__((address_space(3))) void*)(base + f * 1024), 16,
-                uint32_t(afrag32_offset(uint32_t(mb) * 8 + (f >> 2), kb + (f & 3), I, lane)), 0, 0, 0);
-        }
+        const uint32_t a_soff = (st < s_end ? 4 * st : 0) * 1024u;
+        unsigned char* base = abuf + (st % 3) * WIDE_TILE_BYTES + 4 * w * 1024;
+        auto frag = [&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void*)base, 16, a_voff,
+                                                     a_soff, q * 1024, 0);
+        };
+        frag(std::integral_constant<int, 0>{});
+        frag(std::integral_constant<int, 1>{});
+        frag(std::integral_constant<int, 2>{});
+        frag(std::integral_constant<int, 3>{});
     };
     // The compiler does not see the LDS side of these loads, so their
     // completion is awaited by hand: vmcnt(n) with n the vector-memory

@@ -71,31 +71,33 @@ struct Chunk {
     }
 };
 
-// Load chunk g of the tile that starts at byte offset `tile_byte` of `rsrc`.
+// Load chunk g of the tile that starts at byte offset `tile_byte` of `rsrc`:
+// the lane's byte offset is voff + soff, soff a wave-uniform part (an SGPR
+// operand of the load, so a loop can advance it without vector arithmetic).
 template <int K>
-__device__ __forceinline__ void load_chunk(Chunk<K>& c, __amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off) {
-    // byte_off = tile_byte + 4*K*g: 16-byte aligned for K = 4, 8; 4-byte otherwise.
+__device__ __forceinline__ void load_chunk(Chunk<K>& c, __amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff = 0) {
+    // voff + soff = tile_byte + 4*K*g: 16-byte aligned for K = 4, 8; 4-byte otherwise.
     if constexpr (K == 1) {
-        c.d[0] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, byte_off, 0, 0);
+        c.d[0] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff, soff, 0);
     } else if constexpr (K == 2) {
-        u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rsrc, byte_off, 0, 0);
+        u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rsrc, voff, soff, 0);
         c.d[0] = v.x; c.d[1] = v.y;
     } else if constexpr (K == 3) {
-        u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rsrc, byte_off, 0, 0);
+        u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rsrc, voff, soff, 0);
         c.d[0] = v.x; c.d[1] = v.y; c.d[2] = v.z;
     } else {
-        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_off, 0, 0);
+        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0);
         c.d[0] = v.x; c.d[1] = v.y; c.d[2] = v.z; c.d[3] = v.w;
         if constexpr (K == 5) {
-            c.d[4] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, byte_off + 16, 0, 0);
+            c.d[4] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff + 16, soff, 0);
         } else if constexpr (K == 6) {
-            u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rsrc, byte_off + 16, 0, 0);
+            u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rsrc, voff + 16, soff, 0);
             c.d[4] = w.x; c.d[5] = w.y;
         } else if constexpr (K == 7) {
-            u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rsrc, byte_off + 16, 0, 0);
+            u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rsrc, voff + 16, soff, 0);
             c.d[4] = w.x; c.d[5] = w.y; c.d[6] = w.z;
         } else if constexpr (K == 8) {
-            u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_off + 16, 0, 0);
+            u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + 16, soff, 0);
             c.d[4] = w.x; c.d[5] = w.y; c.d[6] = w.z; c.d[7] = w.w;
         }
     }
