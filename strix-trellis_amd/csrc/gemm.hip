@@ -18,7 +18,7 @@ __global__ __launch_bounds__(256) void input_stage_frag_kernel(const float* x, c
                                                                uint32_t nflags) {
     __shared__ __align__(16) _Float16 tile[RB][128 + 8];
     const uint32_t blk = blockIdx.x, rb = blockIdx.y;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     if (blk == 0 && rb == 0)
         for (uint32_t i = tid; i < nflags; i += 256) flags[i] = 0;
     const uint32_t ch = blk * 128;

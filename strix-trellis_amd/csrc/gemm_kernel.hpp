@@ -76,7 +76,7 @@ __global__ __launch_bounds__(2 * BM) void gemm_kernel(GemmArgs a) {
     constexpr int WM = BM / 64, NW = 2 * WM, BPW = GEMM_STAGE_BLOCKS / NW;
     extern __shared__ __align__(16) unsigned char smem[];   // 2 B stages; reused by the epilogue
     const int c = blockIdx.x, mb = blockIdx.y, split = blockIdx.z;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wm = w >> 1, wn = w & 1;
     const int jt = lane >> 3, g = lane & 7;
     // This workgroup's K range: stages (128 channels each) [split * stages, +stages).

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
 // those of the one-row-per-wave fold.
 constexpr uint32_t kPlaneRowsPerWave = 4;
 __global__ __launch_bounds__(GEMV_THREADS) void plane_finish_kernel(GemvArgs a) {
-    const int c = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const uint32_t r0 = (blockIdx.y * GEMV_WAVES + w) * kPlaneRowsPerWave;
     if (r0 >= a.rows) return;
     const ColumnOperands op = column_operands(a.w, c);

@@ -529,7 +529,8 @@ template <int K, int CB, int RT>
 __global__ __launch_bounds__(OWNER_THREADS) void gemv_owner_kernel(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const uint32_t cz = blockIdx.x, z = cz / a.ncg, c = cz - z * a.ncg;
-    const int tid = threadIdx.x, grp = tid >> 8, w = (tid >> 6) & 3, lane = tid & 63;
+    const int tid = threadIdx.x, grp = __builtin_amdgcn_readfirstlane(tid >> 8),
+              w = __builtin_amdgcn_readfirstlane((tid >> 6) & 3), lane = tid & 63;
     const int jt = lane >> 3, g = lane & 7;
     const GroupWeights gw = group_weights(a, int(z));
     const float* x = a.x + z * a.x_group_stride;

@@ -279,7 +279,7 @@ __device__ __forceinline__ void moe_input_stage(int w, int units, const InputLoa
 template <int KG, int KU, int RT>
 __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpert& ex, uint32_t c, uint32_t split,
                                                  uint64_t active, int nrows, _Float16* act, float* red) {
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int jt = lane >> 3, g = lane & 7;
     const uint32_t bps = a.bps_gu, a0 = split * bps;
     const uint32_t act_row = bps * 16;
@@ -372,7 +372,7 @@ void moe_gate_up_kernel(MoeArgs a) {
     float* red = reinterpret_cast<float*>(lds);
     __shared__ uint32_t group_slot[8];
     const uint32_t c = blockIdx.x, split = blockIdx.y;
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot);
     if (!grp.leader || !grp.active) return;
     const uint32_t route = grp.route;
@@ -437,7 +437,7 @@ void moe_gate_up_kernel(MoeArgs a) {
 template <int K, int RT>
 __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert& ex, uint32_t c, uint32_t split,
                                               uint64_t active, int nrows, _Float16* act, float* red) {
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int jt = lane >> 3, g = lane & 7;
     const uint32_t bps = a.bps_d, a0 = split * bps;
     const uint32_t act_row = bps * 16;
@@ -498,7 +498,7 @@ void moe_down_kernel(MoeArgs a) {
     float* red = reinterpret_cast<float*>(lds);
     __shared__ uint32_t finish_mask;
     const uint32_t c = blockIdx.x, split = blockIdx.y;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
     __shared__ uint32_t group_slot[8];
     const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot);
