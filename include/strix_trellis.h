@@ -421,6 +421,13 @@ strix_status strix_tp_moe_plan_create(strix_context context,
 strix_status strix_tp_moe_plan_create_device(strix_context context,
     const strix_tp_moe_device_desc *desc, const strix_stream *stream,
     strix_tp_moe_plan *out);
+/* Split plans: the workspace holds hidden F32 [rows][k][H] and, from the next
+ * 256-byte boundary, P F32 [rows][k][S][I], the down core's per-split partial
+ * sums (S = its split count for input width H).  Every down of a split plan
+ * writes P for each computed route (valid token, non-zero score).  The staged
+ * calls (split plans only): down_core writes P alone, down_finish folds P as
+ * the caller leaves it into the output, down_reference_core recomputes P one
+ * route per workgroup with the same bits. */
 strix_status strix_tp_moe_split_workspace_bytes(strix_context context,
     const strix_tp_moe_desc *desc, uint64_t *out_bytes);
 strix_status strix_tp_moe_plan_create_split(strix_context context,

@@ -55,6 +55,15 @@ strix_status strix_amd_plan_launches(strix_linear_plan plan, uint32_t *launches)
 strix_status strix_amd_swiglu(strix_context context, const float *gate, const float *up, float *hidden,
     uint64_t count, const strix_stream *stream);
 
+/* Workspace bytes of a device-route routed-expert plan, the counterpart of
+ * strix_tp_moe_workspace_bytes (split = 0) and strix_tp_moe_split_workspace_bytes
+ * (split != 0) for strix_tp_moe_device_desc, with the same validation as
+ * strix_tp_moe_plan_create_device.  Plain plans need hidden F32 [rows][k][H];
+ * split plans add P F32 [rows][k][S][I] from the next 256-byte boundary, S the
+ * down core's split count for input width H. */
+strix_status strix_amd_tp_moe_device_workspace_bytes(strix_context context,
+    const strix_tp_moe_device_desc *desc, uint32_t split, uint64_t *out_bytes);
+
 /* Test hook for the prefill GEMM's split-tile handoff (M = 2048-class passes
  * whose 256 x 256 tile count exceeds a multiple of 256 by at most 128).  The
  * second workgroup of a split tile normally continues from the first one's

@@ -99,13 +99,18 @@ def projection(x_rows, w, cache=None, key=None):
                                      rotated=q)["output_fp32"]
 
 
-def down_combine(hidden, experts, ids, scores, alpha=1.0, beta=0.0, old=None, cache=None):
-    """The down half alone: y from given hidden [rows, k, H] (invalid tokens -> NaN rows)."""
-    hidden = np.asarray(hidden, F32)
+def down_finish(partials, experts, ids, scores, alpha=1.0, beta=0.0, old=None):
+    """The down finish from per-split core partials ``partials`` [rows, k, S, I]:
+    per valid token, each non-zero-score slot's core is its S partials summed
+    from +0 in ascending split order (FP32), then that expert's down output
+    stage; the slot sum, alpha/beta and the NaN rows of invalid tokens as in
+    ``down_combine``.  Entries of zero-score slots and invalid tokens are not
+    read.  With S = 1 and the cores of ``linear.core_dot_fp32`` it is
+    ``down_combine`` itself (which calls it so)."""
+    P = np.asarray(partials, F32)
     ids = np.asarray(ids)
     scores = np.asarray(scores, F32)
-    rows, k = ids.shape
-    I = experts[0]["down"][2].shape[0]       # down svh: [I]
+    rows, k, S, I = P.shape
     valid = token_valid(ids, scores, len(experts))
     y = np.empty((rows, I), F32)
     for r in range(rows):
@@ -117,14 +122,49 @@ def down_combine(hidden, experts, ids, scores, alpha=1.0, beta=0.0, old=None, ca
             sc = F32(scores[r, s])
             if sc == 0:
                 continue
-            e = int(ids[r, s])
-            d = projection(hidden[r, s][None, :], experts[e]["down"], cache, (e, "down"))[0]
+            core = np.zeros(I, F32)
+            for u in range(S):
+                core = (core + P[r, s, u]).astype(F32)
+            _, _, svh, bias, _ = experts[int(ids[r, s])]["down"]
+            d = linear.output_stages_fp32(core[None, :], svh, bias)["output_fp32"][0]
             comb = (comb + (sc * d).astype(F32)).astype(F32)
         out = (F32(alpha) * comb).astype(F32)
         if beta != 0:
             out = (out + (F32(beta) * np.asarray(old[r], F32)).astype(F32)).astype(F32)
         y[r] = out
     return y
+
+
+def down_cores(hidden, experts, ids, scores, cache=None):
+    """FP32 down cores [rows, k, I] of the computed routes (valid token,
+    non-zero score) from hidden [rows, k, H]; NaN elsewhere."""
+    hidden = np.asarray(hidden, F32)
+    ids = np.asarray(ids)
+    scores = np.asarray(scores, F32)
+    rows, k = ids.shape
+    I = experts[0]["down"][2].shape[0]       # down svh: [I]
+    valid = token_valid(ids, scores, len(experts))
+    cores = np.full((rows, k, I), np.nan, F32)
+    for r in range(rows):
+        for s in range(k):
+            if not valid[r] or scores[r, s] == 0:
+                continue
+            e = int(ids[r, s])
+            trellis, suh, svh, bias, kk = experts[e]["down"]
+            q = None
+            if cache is not None:
+                q = cache.get((e, "down"))
+                if q is None:
+                    q = cache[(e, "down")] = codec.dequantize_rotated(trellis, kk)
+            st = linear.matmul_fp32_stages(hidden[r, s][None, :], trellis, suh, svh, kk, "mul1", bias, rotated=q)
+            cores[r, s] = st["core_fp32"][0]
+    return cores
+
+
+def down_combine(hidden, experts, ids, scores, alpha=1.0, beta=0.0, old=None, cache=None):
+    """The down half alone: y from given hidden [rows, k, H] (invalid tokens -> NaN rows)."""
+    cores = down_cores(hidden, experts, ids, scores, cache)
+    return down_finish(cores[:, :, None, :], experts, ids, scores, alpha, beta, old)
 
 
 def moe_block(x, experts, ids, scores, alpha=1.0, beta=0.0, old=None, cache=None):

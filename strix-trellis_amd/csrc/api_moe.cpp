@@ -13,7 +13,12 @@
 // Plan-owned device memory (one allocation, freed by destroy): the bank
 // table, the uploaded routes of a host-route plan, the arrival counters (zero
 // between submissions) and the split partial planes.  The caller's workspace
-// holds only hidden F32 [rows][k][H], as in the reference.
+// holds hidden F32 [rows][k][H], as in the reference.  A split plan (the
+// split creators) keeps its down planes in the caller's workspace instead,
+// as P F32 [rows][k][S][I] from the first 256-byte boundary after hidden, the
+// staged checkpoint the reference's split3 plans expose there: every down
+// (fused or staged core) writes P of each computed route, and the staged
+// finish folds P as the caller leaves it.
 #include "api_internal.hpp"
 #include "moe.hpp"
 
@@ -29,6 +34,7 @@ struct strix_tp_moe_plan_impl {
     hipStream_t stream{};
     stx::MoeArgs args{};
     void* device = nullptr;
+    bool split = false;   // P in the caller's workspace; staged down entry points allowed
 };
 
 namespace {
@@ -61,6 +67,9 @@ struct MoeValidated {
     std::vector<float> scores;
     stx::MoeArgs args{};
     uint64_t x_bytes = 0, y_bytes = 0, hidden_bytes = 0;
+    // Split plans: P at p_offset (hidden rounded up to 256 bytes), p_bytes long.
+    uint64_t p_offset = 0, p_bytes = 0;
+    uint64_t workspace_bytes(bool split) const { return split ? p_offset + p_bytes : hidden_bytes; }
 };
 
 // Checks shared by both descriptors: scalars, tensors, experts and geometry.
@@ -134,6 +143,8 @@ strix_status common_check(strix_context c, const D* d, uint64_t routes_per_row, 
     a.x = static_cast<const float*>(d->input.data);
     a.y = static_cast<float*>(d->output.data);
     v.hidden_bytes = rows * routes_per_row * H * sizeof(float);
+    v.p_offset = align_up(v.hidden_bytes);
+    v.p_bytes = stx::moe_down_partial_floats(uint32_t(rows * routes_per_row), I, H) * sizeof(float);
     return STRIX_SUCCESS;
 }
 
@@ -206,9 +217,10 @@ strix_status device_check(strix_context c, const strix_tp_moe_device_desc* d, Mo
 
 // Caller workspace (hidden), device residency of X/Y, then the plan's own memory.
 template <class D>
-strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidated& v, strix_tp_moe_plan* out) {
+strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidated& v, bool split,
+                         strix_tp_moe_plan* out) {
     strix_status s;
-    if (d->workspace_bytes < v.hidden_bytes) return STRIX_ERROR_INSUFFICIENT_BUFFER;
+    if (d->workspace_bytes < v.workspace_bytes(split)) return STRIX_ERROR_INSUFFICIENT_BUFFER;
     if (!d->workspace || !Span(d->workspace, d->workspace_bytes).addressable() ||
         reinterpret_cast<uintptr_t>(d->workspace) % kWorkspaceAlign ||
         Span(d->workspace, d->workspace_bytes).meets(Span(d->input.data, v.x_bytes)) ||
@@ -226,7 +238,8 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     const uint64_t route_bytes = v.ids.empty() ? 0 : 2 * align_up(uint64_t(routes) * 4);
     const uint64_t counter_words = stx::moe_counter_words(a.rows, routes, a.I, a.H);
     const uint64_t counter_bytes = align_up(counter_words * 4);
-    const uint64_t partial_bytes = align_up(stx::moe_partial_floats(routes, a.I, a.H) * 4);
+    const uint64_t partial_bytes = align_up(
+        (split ? stx::moe_gate_up_partial_floats(routes, a.I, a.H) : stx::moe_partial_floats(routes, a.I, a.H)) * 4);
     auto* p = new (std::nothrow) strix_tp_moe_plan_impl;
     if (!p) return STRIX_ERROR_OUT_OF_MEMORY;
     hipError_t e = hipMalloc(&p->device, table_bytes + route_bytes + counter_bytes + partial_bytes);
@@ -251,7 +264,8 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     if (e == hipSuccess) e = stx::launch_fill_u32(a.c_gu, 0, counter_words, hs);
     cursor += counter_bytes;
     a.p_gu = reinterpret_cast<float*>(cursor);
-    a.p_d = a.p_gu + uint64_t(routes) * a.s_gu * 2 * a.H;
+    a.p_d = split ? reinterpret_cast<float*>(static_cast<char*>(d->workspace) + v.p_offset)
+                  : a.p_gu + stx::moe_gate_up_partial_floats(routes, a.I, a.H);
     a.hidden = static_cast<float*>(d->workspace);
     const hipError_t done = hipStreamSynchronize(hs);
     if (e != hipSuccess || done != hipSuccess) {
@@ -262,6 +276,7 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     p->owner = c;
     p->stream = hs;
     p->args = a;
+    p->split = split;
     p->retained = v.retained;
     for (strix_weights w : v.retained) ++w->plans;
     *out = p;
@@ -271,6 +286,63 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
 strix_status plan_ok(strix_tp_moe_plan p) {
     if (!p) return STRIX_ERROR_INVALID_ARGUMENT;
     return on_context_device(p->owner);
+}
+
+// The two creators of each route kind, with and without the split checkpoint.
+strix_status create_host(strix_context c, const strix_tp_moe_desc* d, const strix_stream* stream, bool split,
+                         strix_tp_moe_plan* out) {
+    if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
+    *out = nullptr;
+    strix_status s = on_context_device(c);
+    if (s != STRIX_SUCCESS) return s;
+    hipStream_t hs{};
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
+    try {
+        MoeValidated v;
+        if ((s = host_check(c, d, v)) != STRIX_SUCCESS) return s;
+        return create_plan(c, d, hs, v, split, out);
+    } catch (...) {
+        return STRIX_ERROR_OUT_OF_MEMORY;
+    }
+}
+
+strix_status create_device(strix_context c, const strix_tp_moe_device_desc* d, const strix_stream* stream, bool split,
+                           strix_tp_moe_plan* out) {
+    if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
+    *out = nullptr;
+    strix_status s = on_context_device(c);
+    if (s != STRIX_SUCCESS) return s;
+    hipStream_t hs{};
+    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
+    try {
+        MoeValidated v;
+        if ((s = device_check(c, d, v)) != STRIX_SUCCESS) return s;
+        return create_plan(c, d, hs, v, split, out);
+    } catch (...) {
+        return STRIX_ERROR_OUT_OF_MEMORY;
+    }
+}
+
+strix_status host_workspace(strix_context c, const strix_tp_moe_desc* d, bool split, uint64_t* out) {
+    if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
+    *out = 0;
+    strix_status s = on_context_device(c);
+    if (s != STRIX_SUCCESS) return s;
+    MoeValidated v;
+    try {
+        s = host_check(c, d, v);
+    } catch (...) {
+        return STRIX_ERROR_OUT_OF_MEMORY;
+    }
+    if (s == STRIX_SUCCESS) *out = v.workspace_bytes(split);
+    return s;
+}
+
+// The staged down entry points need a split plan (P in the workspace).
+strix_status split_plan_ok(strix_tp_moe_plan p) {
+    const strix_status s = plan_ok(p);
+    if (s != STRIX_SUCCESS) return s;
+    return p->split ? STRIX_SUCCESS : STRIX_ERROR_INVALID_ARGUMENT;
 }
 }  // namespace
 
@@ -299,66 +371,47 @@ void strix_tp_moe_device_desc_init(strix_tp_moe_device_desc* d) {
 }
 
 strix_status strix_tp_moe_workspace_bytes(strix_context c, const strix_tp_moe_desc* d, uint64_t* out) {
+    return host_workspace(c, d, false, out);
+}
+
+strix_status strix_tp_moe_plan_create(strix_context c, const strix_tp_moe_desc* d, const strix_stream* stream,
+                                      strix_tp_moe_plan* out) {
+    return create_host(c, d, stream, false, out);
+}
+
+strix_status strix_tp_moe_plan_create_device(strix_context c, const strix_tp_moe_device_desc* d,
+                                             const strix_stream* stream, strix_tp_moe_plan* out) {
+    return create_device(c, d, stream, false, out);
+}
+
+// Split plans run the same kernels; their down planes live in the caller's
+// workspace (P after hidden), which the staged down entry points below use.
+strix_status strix_tp_moe_split_workspace_bytes(strix_context c, const strix_tp_moe_desc* d, uint64_t* out) {
+    return host_workspace(c, d, true, out);
+}
+strix_status strix_tp_moe_plan_create_split(strix_context c, const strix_tp_moe_desc* d, const strix_stream* stream,
+                                            strix_tp_moe_plan* out) {
+    return create_host(c, d, stream, true, out);
+}
+strix_status strix_tp_moe_plan_create_device_split(strix_context c, const strix_tp_moe_device_desc* d,
+                                                   const strix_stream* stream, strix_tp_moe_plan* out) {
+    return create_device(c, d, stream, true, out);
+}
+
+strix_status strix_amd_tp_moe_device_workspace_bytes(strix_context c, const strix_tp_moe_device_desc* d,
+                                                     uint32_t split, uint64_t* out) {
     if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
     *out = 0;
     strix_status s = on_context_device(c);
     if (s != STRIX_SUCCESS) return s;
     MoeValidated v;
     try {
-        s = host_check(c, d, v);
+        s = device_check(c, d, v);
     } catch (...) {
         return STRIX_ERROR_OUT_OF_MEMORY;
     }
-    if (s == STRIX_SUCCESS) *out = v.hidden_bytes;
+    if (s == STRIX_SUCCESS) *out = v.workspace_bytes(split != 0);
     return s;
-}
-
-strix_status strix_tp_moe_plan_create(strix_context c, const strix_tp_moe_desc* d, const strix_stream* stream,
-                                      strix_tp_moe_plan* out) {
-    if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
-    *out = nullptr;
-    strix_status s = on_context_device(c);
-    if (s != STRIX_SUCCESS) return s;
-    hipStream_t hs{};
-    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
-    try {
-        MoeValidated v;
-        if ((s = host_check(c, d, v)) != STRIX_SUCCESS) return s;
-        return create_plan(c, d, hs, v, out);
-    } catch (...) {
-        return STRIX_ERROR_OUT_OF_MEMORY;
-    }
-}
-
-strix_status strix_tp_moe_plan_create_device(strix_context c, const strix_tp_moe_device_desc* d,
-                                             const strix_stream* stream, strix_tp_moe_plan* out) {
-    if (!out) return STRIX_ERROR_INVALID_ARGUMENT;
-    *out = nullptr;
-    strix_status s = on_context_device(c);
-    if (s != STRIX_SUCCESS) return s;
-    hipStream_t hs{};
-    if ((s = borrowed_stream(c, stream, hs)) != STRIX_SUCCESS) return s;
-    try {
-        MoeValidated v;
-        if ((s = device_check(c, d, v)) != STRIX_SUCCESS) return s;
-        return create_plan(c, d, hs, v, out);
-    } catch (...) {
-        return STRIX_ERROR_OUT_OF_MEMORY;
-    }
-}
-
-// The split creators select the same two-launch implementation (as the
-// reference does when its split build is off); their workspace is hidden only.
-strix_status strix_tp_moe_split_workspace_bytes(strix_context c, const strix_tp_moe_desc* d, uint64_t* out) {
-    return strix_tp_moe_workspace_bytes(c, d, out);
-}
-strix_status strix_tp_moe_plan_create_split(strix_context c, const strix_tp_moe_desc* d, const strix_stream* stream,
-                                            strix_tp_moe_plan* out) {
-    return strix_tp_moe_plan_create(c, d, stream, out);
-}
-strix_status strix_tp_moe_plan_create_device_split(strix_context c, const strix_tp_moe_device_desc* d,
-                                                   const strix_stream* stream, strix_tp_moe_plan* out) {
-    return strix_tp_moe_plan_create_device(c, d, stream, out);
 }
 
 // A8R is a different arithmetic identity (integer A8 groups); not provided.
@@ -373,10 +426,25 @@ strix_status strix_tp_moe_plan_create_device_a8r(strix_context, const strix_tp_m
     return STRIX_ERROR_NOT_IMPLEMENTED;
 }
 
-// Split-P stage entry points need a split3 plan, which this library does not build.
-strix_status strix_tp_moe_plan_down_core(strix_tp_moe_plan) { return STRIX_ERROR_INVALID_ARGUMENT; }
-strix_status strix_tp_moe_plan_down_finish(strix_tp_moe_plan) { return STRIX_ERROR_INVALID_ARGUMENT; }
-strix_status strix_tp_moe_plan_down_reference_core(strix_tp_moe_plan) { return STRIX_ERROR_INVALID_ARGUMENT; }
+// Staged down of a split plan: the core alone (P of every computed route, each
+// expert group streaming its weights once), the finish alone (from P as it is
+// in the workspace), and the route-alone core (P again, one route per
+// workgroup, without the expert grouping; same bits as the grouped core).
+strix_status strix_tp_moe_plan_down_core(strix_tp_moe_plan p) {
+    const strix_status s = split_plan_ok(p);
+    if (s != STRIX_SUCCESS) return s;
+    return status_of(stx::launch_moe_down_core(p->args, stx::kMoeDownCore, p->stream));
+}
+strix_status strix_tp_moe_plan_down_finish(strix_tp_moe_plan p) {
+    const strix_status s = split_plan_ok(p);
+    if (s != STRIX_SUCCESS) return s;
+    return status_of(stx::launch_moe_down_finish(p->args, p->stream));
+}
+strix_status strix_tp_moe_plan_down_reference_core(strix_tp_moe_plan p) {
+    const strix_status s = split_plan_ok(p);
+    if (s != STRIX_SUCCESS) return s;
+    return status_of(stx::launch_moe_down_core(p->args, stx::kMoeDownRouteCore, p->stream));
+}
 
 strix_status strix_tp_moe_plan_gate_up(strix_tp_moe_plan p) {
     const strix_status s = plan_ok(p);

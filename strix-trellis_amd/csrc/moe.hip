@@ -24,7 +24,38 @@ hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t stream) {
 
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t stream) {
     if (!moe_args_ok(a)) return hipErrorInvalidValue;
-    return down_table[a.down_bits - 2](a, stream);
+    MoeArgs b = a;
+    b.down_mode = kMoeDownFused;
+    return down_table[a.down_bits - 2](b, stream);
+}
+
+hipError_t launch_moe_down_core(const MoeArgs& a, MoeDownMode mode, hipStream_t stream) {
+    if (!moe_args_ok(a) || (mode != kMoeDownCore && mode != kMoeDownRouteCore)) return hipErrorInvalidValue;
+    MoeArgs b = a;
+    b.down_mode = mode;
+    return down_table[a.down_bits - 2](b, stream);
+}
+
+// Staged finish: one wave per (column group, token).  Token validity comes
+// from the same route resolution as the fused launch's; an invalid token gets
+// its NaN row block, a valid one the fused last arrival's ordered finish over
+// the planes as they are in memory.
+__global__ __launch_bounds__(64) void moe_down_finish_kernel(MoeArgs a) {
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const int lane = threadIdx.x;
+    const MoeRoutes rt = moe_routes(a);
+    if ((rt.valid >> (r * a.topk)) & 1) {
+        moe_finish_token(a, r, c, lane);
+    } else {
+        float* yr = a.y + uint64_t(r) * a.y_stride + 128 * c;
+        yr[lane] = yr[lane + 64] = __builtin_bit_cast(float, 0x7fc00000u);
+    }
+}
+
+hipError_t launch_moe_down_finish(const MoeArgs& a, hipStream_t stream) {
+    if (!moe_args_ok(a)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_down_finish_kernel, dim3(a.I / 128, a.rows), dim3(64), 0, stream, a);
+    return hipGetLastError();
 }
 
 __global__ __launch_bounds__(256) void moe_swiglu_kernel(const float* g, const float* u, float* h, uint64_t n) {

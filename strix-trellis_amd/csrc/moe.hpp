@@ -43,6 +43,16 @@ struct MoeArgs {
     uint32_t s_gu, bps_gu, s_d, bps_d;
     uint32_t gate_bits, up_bits, down_bits;
     float alpha, beta;
+    uint32_t down_mode;       // MoeDownMode of a down launch
+};
+
+// What a down launch does.  The staged modes write the per-split partial
+// planes p_d of every computed route (valid token, non-zero score) and
+// nothing else: no arrivals, no output, no NaN rows.
+enum MoeDownMode : uint32_t {
+    kMoeDownFused = 0,       // planes, arrivals, ordered finish by the last arrival
+    kMoeDownCore = 1,        // planes only; each expert group streams its weights once
+    kMoeDownRouteCore = 2,   // planes only; one route per workgroup (no expert grouping)
 };
 
 // Split-K decomposition of one MoE projection with `blocks` 16-channel input
@@ -60,6 +70,14 @@ uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t 
 
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t stream);
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t stream);
+// Staged down: the core alone in `mode` (kMoeDownCore or kMoeDownRouteCore),
+// and the finish alone, which folds the planes p_d as they are in memory
+// (ascending split from +0, output stage, ordered score-weighted slot sum,
+// alpha/beta; NaN rows for invalid tokens), with the fused finish's code.
+hipError_t launch_moe_down_core(const MoeArgs& a, MoeDownMode mode, hipStream_t stream);
+hipError_t launch_moe_down_finish(const MoeArgs& a, hipStream_t stream);
+uint64_t moe_gate_up_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
+uint64_t moe_down_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
 // Diagnostic: h[i] = SwiGLU(g[i], u[i]) with the block's activation arithmetic.
 hipError_t launch_moe_swiglu(const float* g, const float* u, float* h, uint64_t n, hipStream_t stream);
 

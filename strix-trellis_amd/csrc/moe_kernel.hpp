@@ -90,6 +90,34 @@ struct MoeGroup {
     int nan_row;        // else: the invalid token whose NaN rows it writes, or -1
 };
 
+// The routes of all tokens, one lane per route j = r*k + slot (one wave): the
+// lane's bank index, and as wave-wide masks the routes of valid tokens and the
+// routes with a non-zero score.  A token is valid when each of its ids is in
+// the bank and distinct from its other ids, and each score is finite and >= 0.
+struct MoeRoutes {
+    uint32_t id;
+    uint64_t valid, nonzero;
+};
+__device__ __forceinline__ MoeRoutes moe_routes(const MoeArgs& a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t k = a.topk, n = a.rows * k;
+    const bool live = uint32_t(lane) < n;
+    const uint32_t id = ld_global(a.ids + (live ? lane : 0));
+    const float sc = ld_global(a.scores + (live ? lane : 0));
+    const uint32_t row = uint32_t(lane) / k, slot = uint32_t(lane) - row * k;
+    bool ok = live && id < a.bank_count && __builtin_isfinite(sc) && sc >= 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < MOE_MAX_TOPK; ++q) {
+        const uint32_t src = q < k ? row * k + q : uint32_t(lane);
+        const uint32_t other = __shfl(id, int(src & 63), 64);
+        if (q < k && q != slot && other == id) ok = false;
+    }
+    const uint64_t bad = __ballot(live && !ok);
+    const uint64_t row_bits = live ? ((1ull << k) - 1) << (row * k) : 0;   // k <= 8, row*k + k <= 64
+    const bool tv = live && (bad & row_bits) == 0;
+    return {id, __ballot(tv), __ballot(live && sc != 0.0f)};
+}
+
 // Workgroup rank r (grid z, the slowest dimension) takes the r-th expert group
 // in route order: the group led by the r-th leader, a leader being the first
 // route of a valid token to select its expert.  So the workgroups with work
@@ -107,21 +135,11 @@ __device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank)
     const int lane = threadIdx.x & 63;
     const uint32_t k = a.topk, n = a.rows * k;
     const bool live = uint32_t(lane) < n;
-    const uint32_t id = ld_global(a.ids + (live ? lane : 0));
-    const float sc = ld_global(a.scores + (live ? lane : 0));
-    const uint32_t row = uint32_t(lane) / k, slot = uint32_t(lane) - row * k;
-    bool ok = live && id < a.bank_count && __builtin_isfinite(sc) && sc >= 0.0f;
-#pragma unroll
-    for (uint32_t q = 0; q < MOE_MAX_TOPK; ++q) {
-        const uint32_t src = q < k ? row * k + q : uint32_t(lane);
-        const uint32_t other = __shfl(id, int(src & 63), 64);
-        if (q < k && q != slot && other == id) ok = false;
-    }
-    const uint64_t bad = __ballot(live && !ok);
-    const uint64_t row_bits = live ? ((1ull << k) - 1) << (row * k) : 0;   // k <= 8, row*k + k <= 64
-    const bool tv = live && (bad & row_bits) == 0;
-    const uint64_t valid = __ballot(tv);
-    const uint64_t nonzero = __ballot(sc != 0.0f);
+    const uint32_t slot = uint32_t(lane) % k;
+    const MoeRoutes rt = moe_routes(a);
+    const uint32_t id = rt.id;
+    const bool tv = (rt.valid >> lane) & 1;
+    const uint64_t valid = rt.valid, nonzero = rt.nonzero;
     uint64_t rest = valid;
     uint32_t groups = 0;
     for (; rest; ++groups) {
@@ -137,6 +155,18 @@ __device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank)
     if (rank - groups < uint32_t(__builtin_popcountll(firsts)))
         nan_row = int(moe_nth_route(firsts, int(rank - groups)) / k);
     return {0, 0, 0, 0, false, nan_row};
+}
+
+// Route-alone resolution (the reference-core down): workgroup rank j takes
+// route j by itself when its token is valid and its score non-zero, else
+// nothing.  Each route then streams its expert's weights on its own, with the
+// one-row core a grouped route also runs, so its planes must come out the same.
+__device__ __forceinline__ MoeGroup moe_resolve_route(const MoeArgs& a, uint32_t j) {
+    const MoeRoutes rt = moe_routes(a);
+    const uint64_t bit = 1ull << (j & 63);   // j < rows * k <= 64
+    const bool live = j < a.rows * a.topk && (rt.valid & rt.nonzero & bit) != 0;
+    const uint32_t e = uint32_t(__builtin_amdgcn_readlane(int(rt.id), int(j & 63)));
+    return {live ? bit : 0, live ? bit : 0, e, j, live, -1};
 }
 
 // The group with every field read from the first lane: the values are uniform
@@ -158,10 +188,12 @@ __device__ __forceinline__ MoeGroup moe_uniform(const MoeGroup& g) {
 
 // The group of the workgroup (rank = grid z): wave 0 resolves it and shares
 // it through LDS (`slot`, 8 words), one barrier instead of four resolutions,
-// each a few hundred issue slots of a CU that the decode keeps busy.
-__device__ __forceinline__ MoeGroup moe_group_shared(const MoeArgs& a, uint32_t rank, uint32_t* slot) {
+// each a few hundred issue slots of a CU that the decode keeps busy.  With
+// `alone` (uniform) rank j is route j by itself (moe_resolve_route).
+__device__ __forceinline__ MoeGroup moe_group_shared(const MoeArgs& a, uint32_t rank, uint32_t* slot,
+                                                     bool alone = false) {
     if (threadIdx.x < 64) {
-        const MoeGroup g = moe_uniform(moe_resolve(a, rank));
+        const MoeGroup g = moe_uniform(alone ? moe_resolve_route(a, rank) : moe_resolve(a, rank));
         if (threadIdx.x == 0) {
             slot[0] = uint32_t(g.members);
             slot[1] = uint32_t(g.members >> 32);
@@ -490,6 +522,83 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
     __syncthreads();
 }
 
+// Ordered finish of token r over column group c, by one wave (lane 0..63
+// holds columns 128c + lane and +64): each slot's planes p_d summed from +0 in
+// ascending split order, its output stage, RN32(score * value) added in
+// ascending slot order from +0, then alpha/beta.  Lane s fetches slot s's
+// score and expert; then the output-stage operands of every slot and the
+// planes of every slot are loaded together, so a token waits for about three
+// memory round trips however many slots it has.  A zero-score slot loads
+// nothing of its expert and adds no term.  Used by the fused down's last
+// arrival and by the staged finish, so both give the same bits.
+__device__ __forceinline__ void moe_finish_token(const MoeArgs& a, uint32_t r, uint32_t c, int lane) {
+    const uint32_t k = a.topk, I = a.I, S = a.s_d;
+    const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
+    const uint32_t jl = r * k + (uint32_t(lane) < k ? uint32_t(lane) : 0u);
+    const float sc_l = ld_global(a.scores + jl);
+    const MoeExpert& el = a.bank[ld_global(a.ids + jl)];
+    const uint64_t svh_l = reinterpret_cast<uintptr_t>(el.down.svh);
+    const uint64_t bias_l = reinterpret_cast<uintptr_t>(el.down.bias);
+    float sc[MOE_MAX_TOPK], z0[MOE_MAX_TOPK], z1[MOE_MAX_TOPK], b0[MOE_MAX_TOPK], b1[MOE_MAX_TOPK];
+    uint16_t v0[MOE_MAX_TOPK], v1[MOE_MAX_TOPK];
+    bool hb[MOE_MAX_TOPK];
+#pragma unroll
+    for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+        const int sl = uint32_t(s) < k ? s : 0;
+        sc[s] = uint32_t(s) < k ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_l), sl))
+                                : 0.0f;
+        v0[s] = v1[s] = 0;
+        b0[s] = b1[s] = 0.0f;
+        hb[s] = false;
+        z0[s] = z1[s] = 0.0f;
+        if (sc[s] != 0.0f) {
+            const auto* svh = reinterpret_cast<const uint16_t*>(moe_lane64(svh_l, sl));
+            const auto* bias = reinterpret_cast<const float*>(moe_lane64(bias_l, sl));
+            v0[s] = ld_global(svh + n0);
+            v1[s] = ld_global(svh + n1);
+            hb[s] = bias != nullptr;
+            if (hb[s]) {
+                b0[s] = ld_global(bias + n0);
+                b1[s] = ld_global(bias + n1);
+            }
+        }
+    }
+    // Each slot's planes from +0 in ascending split order, all slots per split.
+    for (uint32_t u = 0; u < S; ++u) {
+        float p0[MOE_MAX_TOPK], p1[MOE_MAX_TOPK];
+#pragma unroll
+        for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+            const uint32_t j = r * k + (uint32_t(s) < k ? uint32_t(s) : 0u);
+            const float* p = a.p_d + (uint64_t(j) * S + u) * I + 128 * c;
+            p0[s] = load_coherent(p + lane);
+            p1[s] = load_coherent(p + lane + 64);
+        }
+#pragma unroll
+        for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+            z0[s] = z0[s] + p0[s];
+            z1[s] = z1[s] + p1[s];
+        }
+    }
+    float comb0 = 0.0f, comb1 = 0.0f;
+#pragma unroll
+    for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
+        if (sc[s] == 0.0f) continue;   // also every s >= k
+        h32_wave(z0[s], z1[s]);
+        const float y0 = output_value(z0[s], v0[s], hb[s], b0[s], 1.0f, 0.0f, nullptr);
+        const float y1 = output_value(z1[s], v1[s], hb[s], b1[s], 1.0f, 0.0f, nullptr);
+        comb0 = rn32(comb0 + rn32(sc[s] * y0));
+        comb1 = rn32(comb1 + rn32(sc[s] * y1));
+    }
+    float* yr = a.y + uint64_t(r) * a.y_stride;
+    float o0 = rn32(a.alpha * comb0), o1 = rn32(a.alpha * comb1);
+    if (a.beta != 0.0f) {
+        o0 = rn32(o0 + rn32(a.beta * ld_global(yr + n0)));
+        o1 = rn32(o1 + rn32(a.beta * ld_global(yr + n1)));
+    }
+    *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
+    *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+}
+
 template <int K>
 __global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(moe_waves_per_eu(K, 1))))
 void moe_down_kernel(MoeArgs a) {
@@ -501,10 +610,11 @@ void moe_down_kernel(MoeArgs a) {
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
     __shared__ uint32_t group_slot[8];
-    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot);
+    const bool staged = a.down_mode != kMoeDownFused;   // a kernel argument: uniform
+    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot, a.down_mode == kMoeDownRouteCore);
     if (!grp.leader) {
         // One workgroup per (invalid token, column group) writes its NaN row block.
-        if (grp.nan_row >= 0 && split == 0 && tid < 128)
+        if (!staged && grp.nan_row >= 0 && split == 0 && tid < 128)
             a.y[uint64_t(grp.nan_row) * a.y_stride + 128 * c + tid] = __builtin_bit_cast(float, 0x7fc00000u);
         return;
     }
@@ -525,6 +635,7 @@ void moe_down_kernel(MoeArgs a) {
             store_coherent(a.p_d + (uint64_t(j) * S + split) * I + 128 * c + n, v);
         }
     }
+    if (staged) return;   // the planes are the staged core's result
     moe_release();
     // One arrival per member route (one route per token), lanes in parallel.
     const uint32_t expected = k * S;
@@ -547,79 +658,12 @@ void moe_down_kernel(MoeArgs a) {
     if (!fm) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-    // Tokens whose last arrival this was: ordered slot fold, alpha/beta.  Lane
-    // s fetches slot s's score and expert; then the output-stage operands of
-    // every slot and the planes of every slot are loaded together, so a token
-    // waits for about three memory round trips however many slots it has.  A
-    // zero-score slot loads nothing of its expert and adds no term.
-    const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
+    // Tokens whose last arrival this was, one per wave (moe_finish_token).
     int q = 0;
     for (uint32_t m = fm; m; m &= m - 1, ++q) {
         if (q % GEMV_WAVES != w) continue;
         const uint32_t r = uint32_t(__builtin_ctz(m));
-        const uint32_t jl = r * k + (uint32_t(lane) < k ? uint32_t(lane) : 0u);
-        const float sc_l = ld_global(a.scores + jl);
-        const MoeExpert& el = a.bank[ld_global(a.ids + jl)];
-        const uint64_t svh_l = reinterpret_cast<uintptr_t>(el.down.svh);
-        const uint64_t bias_l = reinterpret_cast<uintptr_t>(el.down.bias);
-        float sc[MOE_MAX_TOPK], z0[MOE_MAX_TOPK], z1[MOE_MAX_TOPK], b0[MOE_MAX_TOPK], b1[MOE_MAX_TOPK];
-        uint16_t v0[MOE_MAX_TOPK], v1[MOE_MAX_TOPK];
-        bool hb[MOE_MAX_TOPK];
-#pragma unroll
-        for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
-            const int sl = uint32_t(s) < k ? s : 0;
-            sc[s] = uint32_t(s) < k ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_l), sl))
-                                    : 0.0f;
-            v0[s] = v1[s] = 0;
-            b0[s] = b1[s] = 0.0f;
-            hb[s] = false;
-            z0[s] = z1[s] = 0.0f;
-            if (sc[s] != 0.0f) {
-                const auto* svh = reinterpret_cast<const uint16_t*>(moe_lane64(svh_l, sl));
-                const auto* bias = reinterpret_cast<const float*>(moe_lane64(bias_l, sl));
-                v0[s] = ld_global(svh + n0);
-                v1[s] = ld_global(svh + n1);
-                hb[s] = bias != nullptr;
-                if (hb[s]) {
-                    b0[s] = ld_global(bias + n0);
-                    b1[s] = ld_global(bias + n1);
-                }
-            }
-        }
-        // Each slot's planes from +0 in ascending split order, all slots per split.
-        for (uint32_t u = 0; u < S; ++u) {
-            float p0[MOE_MAX_TOPK], p1[MOE_MAX_TOPK];
-#pragma unroll
-            for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
-                const uint32_t j = r * k + (uint32_t(s) < k ? uint32_t(s) : 0u);
-                const float* p = a.p_d + (uint64_t(j) * S + u) * I + 128 * c;
-                p0[s] = load_coherent(p + lane);
-                p1[s] = load_coherent(p + lane + 64);
-            }
-#pragma unroll
-            for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
-                z0[s] = z0[s] + p0[s];
-                z1[s] = z1[s] + p1[s];
-            }
-        }
-        float comb0 = 0.0f, comb1 = 0.0f;
-#pragma unroll
-        for (int s = 0; s < int(MOE_MAX_TOPK); ++s) {
-            if (sc[s] == 0.0f) continue;   // also every s >= k
-            h32_wave(z0[s], z1[s]);
-            const float y0 = output_value(z0[s], v0[s], hb[s], b0[s], 1.0f, 0.0f, nullptr);
-            const float y1 = output_value(z1[s], v1[s], hb[s], b1[s], 1.0f, 0.0f, nullptr);
-            comb0 = rn32(comb0 + rn32(sc[s] * y0));
-            comb1 = rn32(comb1 + rn32(sc[s] * y1));
-        }
-        float* yr = a.y + uint64_t(r) * a.y_stride;
-        float o0 = rn32(a.alpha * comb0), o1 = rn32(a.alpha * comb1);
-        if (a.beta != 0.0f) {
-            o0 = rn32(o0 + rn32(a.beta * ld_global(yr + n0)));
-            o1 = rn32(o1 + rn32(a.beta * ld_global(yr + n1)));
-        }
-        *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
-        *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+        moe_finish_token(a, r, c, lane);
         if (lane == 0) __hip_atomic_store(a.c_d + uint64_t(r) * (I >> 7) + c, 0u, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
     }

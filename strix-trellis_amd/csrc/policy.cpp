@@ -206,9 +206,16 @@ MoeSplit moe_split(uint32_t input, uint32_t max_bps) {
     return {bps, blocks / bps};
 }
 
+uint64_t moe_gate_up_partial_floats(uint32_t routes, uint32_t I, uint32_t H) {
+    return uint64_t(routes) * moe_split(I, MOE_GU_MAX_BPS).splits * 2 * H;
+}
+
+uint64_t moe_down_partial_floats(uint32_t routes, uint32_t I, uint32_t H) {
+    return uint64_t(routes) * moe_split(H, MOE_D_MAX_BPS).splits * I;
+}
+
 uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H) {
-    return uint64_t(routes) * moe_split(I, MOE_GU_MAX_BPS).splits * 2 * H +
-           uint64_t(routes) * moe_split(H, MOE_D_MAX_BPS).splits * I;
+    return moe_gate_up_partial_floats(routes, I, H) + moe_down_partial_floats(routes, I, H);
 }
 
 uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H) {

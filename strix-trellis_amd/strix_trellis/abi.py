@@ -175,6 +175,9 @@ _PROTOTYPES = {
     "strix_tp_moe_plan_submit": (_S, [vp]),
     "strix_tp_moe_plan_gate_up": (_S, [vp]),
     "strix_tp_moe_plan_down": (_S, [vp]),
+    "strix_tp_moe_plan_down_core": (_S, [vp]),
+    "strix_tp_moe_plan_down_finish": (_S, [vp]),
+    "strix_tp_moe_plan_down_reference_core": (_S, [vp]),
     "strix_tp_moe_plan_destroy": (_S, [vp]),
     "strix_amd_decode": (_S, [vp, vp, u64, C.POINTER(Stream)]),
     "strix_amd_input_stage": (_S, [vp, vp, u64, vp, u64, C.POINTER(Stream)]),
@@ -183,6 +186,7 @@ _PROTOTYPES = {
     "strix_amd_plan_launches": (_S, [vp, C.POINTER(u32)]),
     "strix_amd_gemm_splits": (_S, [vp, u64, C.POINTER(u32)]),
     "strix_amd_swiglu": (_S, [vp, vp, vp, vp, u64, C.POINTER(Stream)]),
+    "strix_amd_tp_moe_device_workspace_bytes": (_S, [vp, C.POINTER(TpMoeDeviceDesc), u32, C.POINTER(u64)]),
     "strix_amd_set_gemm_handoff": (_S, [vp, u32]),
     "strix_amd_set_gemv_poll_limit": (_S, [vp, u32]),
     "strix_amd_plan_status": (_S, [vp, u32, C.POINTER(u32)]),

@@ -385,6 +385,10 @@ class MoePlan:
 
     def __init__(self, ctx, experts, x, y, ids=None, scores=None, expert_ids=None, device_ids=None,
                  device_scores=None, alpha=1.0, beta=0.0, workspace=None, stream=None, split=False):
+        """``split`` builds a split plan: its workspace holds hidden, then the
+        down core's per-split partials P [rows, k, S, I] (``self.partials``),
+        which the staged ``down_core`` / ``down_finish`` /
+        ``down_reference_core`` write and read."""
         self.lib = ctx.lib
         torch = _t()
         n = len(experts)
@@ -414,14 +418,28 @@ class MoePlan:
                            route_scores=C.c_void_p(device_scores.data_ptr()),
                            route_scores_bytes=device_scores.numel() * 4, alpha=alpha, beta=beta)
             k = device_ids.numel() // rows
-        H = experts[0][0].output
+        H, I = experts[0][0].output, experts[0][0].input
+        need = C.c_uint64(rows * k * H * 4)
+        if split:
+            if device_ids is None:
+                abi.check(self.lib.strix_tp_moe_split_workspace_bytes(ctx.handle, C.byref(d), C.byref(need)),
+                          "strix_tp_moe_split_workspace_bytes")
+            else:
+                abi.check(self.lib.strix_amd_tp_moe_device_workspace_bytes(ctx.handle, C.byref(d), 1,
+                                                                           C.byref(need)),
+                          "strix_amd_tp_moe_device_workspace_bytes")
         if workspace is None:
-            workspace = _on_stream(torch.empty(rows * k * H, dtype=torch.float32, device=x.device), stream)
+            workspace = _on_stream(torch.empty(need.value // 4, dtype=torch.float32, device=x.device), stream)
         d.workspace = C.c_void_p(workspace.data_ptr())
         d.workspace_bytes = workspace.numel() * workspace.element_size()
         keep.append(workspace)
         self.workspace = workspace
         self.hidden = workspace[:rows * k * H].view(rows, k, H)
+        self.partials = None
+        if split:
+            off = (rows * k * H * 4 + 255) // 256 * 256 // 4
+            splits = (need.value // 4 - off) // (rows * k * I)
+            self.partials = workspace[off:off + rows * k * splits * I].view(rows, k, splits, I)
         self._keep = keep
         h = C.c_void_p()
         if device_ids is None:
@@ -439,6 +457,16 @@ class MoePlan:
 
     def down(self):
         abi.check(self.lib.strix_tp_moe_plan_down(self.handle), "strix_tp_moe_plan_down")
+
+    def down_core(self):
+        abi.check(self.lib.strix_tp_moe_plan_down_core(self.handle), "strix_tp_moe_plan_down_core")
+
+    def down_finish(self):
+        abi.check(self.lib.strix_tp_moe_plan_down_finish(self.handle), "strix_tp_moe_plan_down_finish")
+
+    def down_reference_core(self):
+        abi.check(self.lib.strix_tp_moe_plan_down_reference_core(self.handle),
+                  "strix_tp_moe_plan_down_reference_core")
 
     def destroy(self):
         if self.handle:

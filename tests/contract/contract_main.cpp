@@ -556,8 +556,51 @@ static void moe_plan(strix_context c, hipStream_t hs) {
     fake::launch_fail_at = 1;   // the down launch
     STATUS(strix_tp_moe_plan_submit(p), STRIX_ERROR_BACKEND);
     fake::reset_failures();
+    // The staged down checkpoints need a split plan.
+    STATUS(strix_tp_moe_plan_down_core(p), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_tp_moe_plan_down_finish(p), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_tp_moe_plan_down_reference_core(p), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_tp_moe_plan_down_core(nullptr), STRIX_ERROR_INVALID_ARGUMENT);
     STATUS(strix_tp_moe_plan_destroy(p), STRIX_SUCCESS);
     CHECK(fake::live.size() == live0);
+
+    // Split plan: P [rows][k][S][I] after hidden rounded up to 256 bytes, the
+    // down planes of every launch (checked in device memory by the launchers).
+    uint64_t split_need = 0;
+    STATUS(strix_tp_moe_split_workspace_bytes(c, &d, &split_need), STRIX_SUCCESS);
+    const uint64_t hidden_bytes = uint64_t(rows) * k * H * 4;
+    const uint32_t sd = stx::moe_split(H, stx::MOE_D_MAX_BPS).splits;
+    CHECK(split_need == ((hidden_bytes + 255) & ~uint64_t(255)) + uint64_t(rows) * k * sd * I * 4);
+    STATUS(strix_tp_moe_plan_create_split(c, &d, &st, &p), STRIX_ERROR_INSUFFICIENT_BUFFER);   // hidden only
+    CHECK(p == nullptr && fake::live.size() == live0);
+    void* plain_ws = d.workspace;
+    void* split_ws = device_alloc(split_need);
+    d.workspace = split_ws;
+    d.workspace_bytes = split_need - 4;
+    STATUS(strix_tp_moe_plan_create_split(c, &d, &st, &p), STRIX_ERROR_INSUFFICIENT_BUFFER);
+    d.workspace_bytes = split_need;
+    const size_t live1 = fake::live.size();
+    STATUS(strix_tp_moe_plan_create_split(c, &d, &st, &p), STRIX_SUCCESS);
+    CHECK(fake::live.size() == live1 + 1);
+    fake::launches.clear();
+    {
+        const fake::Counters before = fake::n;
+        STATUS(strix_tp_moe_plan_submit(p), STRIX_SUCCESS);
+        STATUS(strix_tp_moe_plan_down_core(p), STRIX_SUCCESS);
+        STATUS(strix_tp_moe_plan_down_finish(p), STRIX_SUCCESS);
+        STATUS(strix_tp_moe_plan_down_reference_core(p), STRIX_SUCCESS);
+        check_quiet_since(before);
+    }
+    CHECK(fake::launches.size() == 5 && fake::launches[2].name == "moe_down_core" &&
+          fake::launches[3].name == "moe_down_finish" && fake::launches[4].name == "moe_down_route_core");
+    fake::launch_fail_at = 0;
+    STATUS(strix_tp_moe_plan_down_finish(p), STRIX_ERROR_BACKEND);
+    fake::reset_failures();
+    STATUS(strix_tp_moe_plan_destroy(p), STRIX_SUCCESS);
+    CHECK(fake::live.size() == live1);
+    CHECK(hipFree(split_ws) == hipSuccess);
+    d.workspace = plain_ws;
+    d.workspace_bytes = need;
     for (strix_weights w : ws) STATUS(strix_weights_destroy(w), STRIX_SUCCESS);
     for (void* q : {x, y, d.workspace}) CHECK(hipFree(q) == hipSuccess);
 }

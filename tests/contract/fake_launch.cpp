@@ -217,6 +217,20 @@ hipError_t launch_moe_down(const MoeArgs& a, hipStream_t s) {
     return fake::launch_result();
 }
 
+hipError_t launch_moe_down_core(const MoeArgs& a, MoeDownMode mode, hipStream_t s) {
+    check_moe(a, false, "launch_moe_down_core");
+    require(mode == kMoeDownCore || mode == kMoeDownRouteCore, "staged down mode", "launch_moe_down_core");
+    record(mode == kMoeDownCore ? "moe_down_core" : "moe_down_route_core", a.rows, nullptr, nullptr, s, a.alpha,
+           a.beta);
+    return fake::launch_result();
+}
+
+hipError_t launch_moe_down_finish(const MoeArgs& a, hipStream_t s) {
+    check_moe(a, false, "launch_moe_down_finish");
+    record("moe_down_finish", a.rows, nullptr, nullptr, s, a.alpha, a.beta);
+    return fake::launch_result();
+}
+
 hipError_t launch_moe_swiglu(const float* g, const float* u, float* h, uint64_t count, hipStream_t s) {
     require(fake::in_live_block(g, count * 4) && fake::in_live_block(u, count * 4) &&
                 fake::in_live_block(h, count * 4),

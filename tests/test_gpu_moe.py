@@ -250,3 +250,111 @@ def test_staged_entry_points_and_validation(ctx):
                         device_scores=_dev(sc9))
     _destroy(ws)
     _destroy(wbig)
+
+
+def _same_bits(a, b):
+    """Bitwise equality where NaN matches NaN."""
+    return bool(np.all((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))))
+
+
+def test_split_plan_checkpoints(ctx):
+    """Split plans keep the down core's per-split partials P [rows, k, S, I] in
+    the workspace.  The fused down and the staged core write the same P; the
+    route-alone core writes it again without the expert grouping; the staged
+    finish reproduces the fused output from P and, on any P, the oracle's
+    finish bit for bit; P's split sums meet the core's FP64 bound.  Plain plans
+    refuse the staged down."""
+    from oracle import codec, linear
+    E, I, H, R, k = 6, 256, 2048, 3, 3
+    print(f"moe split plan E={E} I={I} H={H} R={R} k={k}", flush=True)
+    bank = synth.moe_bank(E, I, H, 2, 555, bias=True)
+    ws = _weights(ctx, bank)
+    ids, sc = synth.routes(R, E, k, 556)
+    sc[0, 1] = 0.0            # a skipped slot
+    ids[2, 2] = ids[2, 0]     # token 2 is invalid: NaN row
+    x = synth.activations(R, I, 557)
+    routed = np.ones((R, k), bool)
+    routed[0, 1] = False
+    routed[2] = False
+    y_plain, _ = _run(ctx, ws, x, ids, sc, device=True)
+    assert np.isnan(y_plain[2]).all() and np.isfinite(y_plain[:2]).all()
+
+    y = torch.full((R, I), float("nan"), device=DEV)
+    plan = runtime.MoePlan(ctx, ws, _dev(x), y, device_ids=_dev(ids.astype(np.int32)), device_scores=_dev(sc),
+                           split=True)
+    S = plan.partials.shape[2]
+    assert plan.partials.shape == (R, k, S, I) and S >= 2
+    plan.submit()
+    torch.cuda.synchronize()
+    y_full, P_full = y.cpu().numpy(), plan.partials.cpu().numpy()
+    hidden = plan.hidden.cpu().numpy()
+    assert _same_bits(y_full, y_plain)
+    assert np.isfinite(P_full[routed]).all()
+
+    # the staged core writes the same P for every computed route, nothing else
+    plan.partials.fill_(float("nan"))
+    plan.gate_up()
+    plan.down_core()
+    torch.cuda.synchronize()
+    P_core = plan.partials.cpu().numpy()
+    assert _same_bits(P_core[routed], P_full[routed])
+    assert np.isnan(P_core[~routed]).all()
+    # the staged finish from P gives the fused output, NaN row included
+    y.fill_(0.0)
+    plan.down_finish()
+    torch.cuda.synchronize()
+    assert _same_bits(y.cpu().numpy(), y_full)
+    # route-alone core: the same P without the expert grouping
+    plan.partials.fill_(float("nan"))
+    plan.down_reference_core()
+    torch.cuda.synchronize()
+    P_ref = plan.partials.cpu().numpy()
+    assert _same_bits(P_ref[routed], P_full[routed])
+    assert np.isnan(P_ref[~routed]).all()
+
+    # P against the oracle: each computed route's split sum (ascending from +0)
+    # within the FP64 bound of its core, from the GPU's own hidden
+    for r in range(R):
+        for s in range(k):
+            if not routed[r, s]:
+                continue
+            tr, suh, _, _, kk = bank[int(ids[r, s])]["down"]
+            a = linear.input_stages_fp32(hidden[r, s][None, :], suh)["core_input_fp16"]
+            q = codec.dequantize_rotated(tr, kk)
+            fold = np.zeros(I, np.float32)
+            for u in range(S):
+                fold = (fold + P_full[r, s, u]).astype(np.float32)
+            assert np.all(np.abs(fold - linear.core_exact_f64(a, q)[0]) <= linear.gamma_bound(a, q)[0]), (r, s)
+
+    # the staged finish on an arbitrary P follows the oracle's finish bit for bit
+    g = synth.rng(558)
+    Q = (g.standard_normal((R, k, S, I)) * 50).astype(np.float32)
+    plan.partials.copy_(_dev(Q))
+    y.fill_(0.0)
+    plan.down_finish()
+    torch.cuda.synchronize()
+    assert _same_bits(y.cpu().numpy(), moe.down_finish(Q, bank, ids, sc))
+    plan.destroy()
+
+    # a host-route split plan over the used experts gives the same P and output
+    used = sorted(set(ids[:2].ravel().tolist()))
+    remap = {e: i for i, e in enumerate(used)}
+    rows_ok = [0, 1]
+    ih = np.vectorize(remap.get)(ids[rows_ok]).astype(np.uint32)
+    yh = torch.full((2, I), float("nan"), device=DEV)
+    hp = runtime.MoePlan(ctx, [ws[e] for e in used], _dev(x[rows_ok]), yh, ids=ih, scores=sc[rows_ok], split=True)
+    hp.submit()
+    torch.cuda.synchronize()
+    assert _same_bits(yh.cpu().numpy(), y_full[rows_ok])
+    assert _same_bits(hp.partials.cpu().numpy()[routed[rows_ok]], P_full[rows_ok][routed[rows_ok]])
+    hp.destroy()
+
+    # plain plans have no P: the staged down is refused
+    yp = torch.empty((R, I), device=DEV)
+    pp = runtime.MoePlan(ctx, ws, _dev(x), yp, device_ids=_dev(ids.astype(np.int32)), device_scores=_dev(sc))
+    assert pp.partials is None
+    for fn in (pp.down_core, pp.down_finish, pp.down_reference_core):
+        with pytest.raises(abi.StrixError):
+            fn()
+    pp.destroy()
+    _destroy(ws)

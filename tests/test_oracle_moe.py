@@ -115,3 +115,67 @@ def test_block_identities():
     ref = (np.float32(0.5) * y).astype(np.float32)
     ref = (ref + (np.float32(-2.0) * old).astype(np.float32)).astype(np.float32)
     assert np.array_equal(yab.view(np.uint32), ref.view(np.uint32))
+
+
+def test_down_finish_from_split_partials():
+    """down_finish over S > 1 partials: exact splits of each core give the S = 1
+    bits; the split sum starts at +0 in ascending order; entries of skipped
+    routes are never read; a brute-force restatement over scalars agrees."""
+    bank, ids, sc, x = _tiny(R=3, k=3, E=5)
+    sc = sc.copy()
+    sc[1, 2] = 0.0                          # a skipped slot
+    ids = ids.copy()
+    ids[2, 1] = ids[2, 0]                   # token 2 invalid (repeated id)
+    _, hidden = moe.moe_block(x, bank, ids, sc, cache={})
+    cores = moe.down_cores(hidden, bank, ids, sc)
+    y1 = moe.down_combine(hidden, bank, ids, sc)
+    assert np.array_equal(moe.down_finish(cores[:, :, None, :], bank, ids, sc).view(np.uint32), y1.view(np.uint32))
+    assert np.isnan(y1[2]).all() and np.isfinite(y1[:2]).all()
+    # Exact three-way splits: each core c as its top 8, next 8 and last 8
+    # significant bits (same sign), so every partial sum is exact and the fold
+    # reproduces c.
+    g = synth.rng(77)
+    S = 3
+    P = np.zeros(cores.shape[:2] + (S, cores.shape[2]), np.float32)
+    live = np.isfinite(cores)
+    c64 = np.where(live, cores, 0).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(np.abs(c64), 1e-30)))
+    hi = np.trunc(np.ldexp(c64, (7 - e).astype(np.int64)))
+    hi = np.ldexp(hi, (e - 7).astype(np.int64))
+    mid = np.ldexp(np.trunc(np.ldexp(c64 - hi, (15 - e).astype(np.int64))), (e - 15).astype(np.int64))
+    P[:, :, 0] = hi.astype(np.float32)
+    P[:, :, 1] = mid.astype(np.float32)
+    P[:, :, 2] = (c64 - hi - mid).astype(np.float32)
+    assert np.array_equal(P.astype(np.float64).sum(axis=2), c64)
+    fold = ((P[:, :, 0] + P[:, :, 1]).astype(np.float32) + P[:, :, 2]).astype(np.float32)
+    assert np.array_equal(fold[live].view(np.uint32), cores[live].view(np.uint32))
+    # entries of the skipped slot and the invalid token are NaN: never read
+    routed = live[:, :, 0]
+    assert routed.sum() == routed.size - 1 - ids.shape[1]
+    P[~routed] = np.nan
+    yS = moe.down_finish(P, bank, ids, sc)
+    same = (yS.view(np.uint32) == y1.view(np.uint32)) | (np.isnan(yS) & np.isnan(y1))
+    assert same.all()
+    # the split order is ascending from +0: a restatement over scalars for one
+    # output of one token, against an order where the rounding differs
+    Q = g.standard_normal(P.shape).astype(np.float32) * np.float32(1e3)
+    Q[1, 0, 0] = np.float32(1e8)
+    Q[1, 0, 1] = np.float32(-1e8)
+    Q[1, 0, 2] = np.float32(0.75)
+    Q[~routed] = np.nan
+    yq = moe.down_finish(Q, bank, ids, sc)
+    r = 1
+    comb = np.zeros(yq.shape[1], np.float32)
+    for s in range(3):
+        if sc[r, s] == 0:
+            continue
+        core = np.zeros(Q.shape[3], np.float32)
+        for u in range(S):
+            core = (core + Q[r, s, u]).astype(np.float32)
+        _, _, svh, bias, _ = bank[int(ids[r, s])]["down"]
+        d = linear.output_stages_fp32(core[None, :], svh, bias)["output_fp32"][0]
+        comb = (comb + (np.float32(sc[r, s]) * d).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(yq[r].view(np.uint32), comb.view(np.uint32))
+    rev = Q.copy()
+    rev[:, :, [0, 1, 2]] = Q[:, :, [2, 1, 0]]
+    assert not np.array_equal(moe.down_finish(rev, bank, ids, sc)[r], yq[r])
