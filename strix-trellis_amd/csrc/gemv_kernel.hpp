@@ -163,6 +163,14 @@ __device__ __forceinline__ uint32_t load_epoch(const uint32_t* p) {
     return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A wave-uniform value loaded earlier into a vector register, read into a
+// scalar one here.  The empty asm keeps the value in its vector register up to
+// this point, so the load's wait lands here instead of right after the load.
+__device__ __forceinline__ uint32_t uniform_late(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return uint32_t(__builtin_amdgcn_readfirstlane(int(v)));
+}
+
 // Plane words of column group cz in set k: [S-1][rows][128].
 __device__ __forceinline__ float* fused_planes(const GemvArgs& a, uint32_t cz, uint32_t k) {
     const uint64_t per_cg = uint64_t(a.splits - 1) * a.rows * 128u;
@@ -395,7 +403,10 @@ void gemv_kernel(GemvArgs a) {
     // every other split publishes a plane.
     const bool fused = a.mode == 1 && a.splits > 1;
     const bool finisher = a.splits == 1 || (fused && uint32_t(s) == a.splits - 1);
-    const uint32_t epoch = fused ? load_epoch(a.state.epochs + place.cz) : 0u;
+    // The loaded word stays in a vector register until the planes are chosen
+    // (uniform_late below): read into a scalar register at once, the load's
+    // wait would sit here, ahead of every input and weight load.
+    const uint32_t epoch_v = fused ? load_epoch(a.state.epochs + place.cz) : 0u;
 
     // Prologue: FP16 core input of this split's channels, one 128-block unit
     // per wave at a time, the loads of kUnits units per wave in flight
@@ -469,6 +480,7 @@ void gemv_kernel(GemvArgs a) {
     // Wave partials -> LDS, added in wave order.
     mfma_partials<RT>(acc, red + w * RT * 128);
     lds_barrier();
+    const uint32_t epoch = uniform_late(epoch_v);
     float* cur = fused ? fused_planes(a, place.cz, epoch & 1u) : nullptr;
     float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
     for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
