@@ -48,11 +48,13 @@ uint64_t linear_workspace_bytes(const DeviceWeights& w, uint64_t rows);
 //   planes  two sets of partial sums of splits 0..S-2, per column group
 //           ([2][groups * N/128][S-1][rows][128] F32).
 // Created with status and epochs 0 and every plane word GEMV_PLANE_EMPTY.  A
-// launch of column group g with epoch e uses set e & 1: its finisher polls
-// that set until no word is EMPTY, and re-arms (EMPTY-fills) the other set,
-// which the previous launch used and which no workgroup of this launch
-// touches; then it advances epochs[g].  A partial published late (after a
-// finisher gave up) lands in a set the next launch leaves alone and re-arms.
+// launch of column group g with epoch e uses set e & 1: each split publishes
+// its plane there and re-arms (EMPTY-fills) its plane of the other set, which
+// the previous launch used and which nothing of this launch reads; the
+// finisher polls set e & 1 until no word is EMPTY, then advances epochs[g].
+// A partial published late (after a finisher gave up, before its launch
+// ended) lands in a set the next launch does not read, and whose planes that
+// launch's splits re-arm.
 struct FusedState {
     uint32_t* status = nullptr;
     uint32_t* epochs = nullptr;

@@ -143,10 +143,11 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
 //
 // Every workgroup of column group cz reads epochs[cz] when it starts; the
 // launch uses plane set epochs[cz] & 1.  Splits 0..S-2 publish their partial
-// sums into it and exit.  The workgroup of split S-1 (dispatched after them,
-// on the same XCD) re-arms the other set, loads its set's words until none is
-// EMPTY, folds them in ascending split order with its own sums (in LDS, split
-// S-1) last, finishes the output and advances epochs[cz].
+// sums into it, re-arm their own plane of the other set (the previous
+// launch's, which has ended: nothing of this launch reads it) and exit.  The
+// workgroup of split S-1 (dispatched after them) loads its set's words until
+// none is EMPTY, folds them in ascending split order with its own sums (in
+// LDS, split S-1) last, finishes the output and advances epochs[cz].
 //   * An aligned 32-bit store is seen whole or not at all.  No partial sum can
 //     be the EMPTY pattern: FP16 operands make every NaN the core produces
 //     carry 13 zero low bits, and EMPTY has none.
@@ -154,8 +155,8 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
 //     written through to memory, a poll reads past the L1.
 //   * The poll is bounded: a finisher that gives up writes NaN outputs, sets
 //     GEMV_STATUS_GAVE_UP in the sticky status word and still advances the
-//     epoch; partials that land afterwards sit in a set the next launch does
-//     not read, and its finisher re-arms that set.
+//     epoch; partials that land afterwards (before this launch ends) sit in a
+//     set the next launch does not read, and its splits re-arm that set.
 //   * Its dependencies were dispatched before it and at most ncg * groups
 //     finishers exist, so the wait always ends.
 // ---------------------------------------------------------------------------
@@ -185,14 +186,12 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // `own` holds this workgroup's [rows][128] sums (split S-1); `cur` the
-// column group's planes of this launch's set, `prev` those of the other set.
+// column group's planes of this launch's set.
 // Wave w takes rows w, w+4 (RPW = 1 or 2 rows per wave): the loads of both
-// rows are issued in one poll round (kFoldBatch / RPW splits per round).  On CDNA a wave's stores count in the
-// same vmcnt as its loads, so the re-arm stores are issued after the polls
-// (a wait for a poll would otherwise also wait for them to be written).
+// rows are issued in one poll round (kFoldBatch / RPW splits per round).
 template <int RPW>
 __device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeights& gw, const ColumnOperands& op,
-                                              float* y, int c, const float* own, const float* cur, float* prev,
+                                              float* y, int c, const float* own, const float* cur,
                                               uint32_t epoch, uint32_t cz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int others = int(a.splits) - 1;
@@ -266,11 +265,7 @@ __device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeig
             *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
         }
     }
-    // Re-arm the previous launch's set (no workgroup of this launch reads or
-    // writes it) and advance the epoch.
-    const float empty = __builtin_bit_cast(float, GEMV_PLANE_EMPTY);
-    const uint32_t words = uint32_t(others) * a.rows * 128u;
-    for (uint32_t i = threadIdx.x; i < words; i += GEMV_THREADS) store_coherent(prev + i, empty);
+    // Advance the epoch (the splits have re-armed the other set).
     if (gave_up && lane == 0)
         __hip_atomic_fetch_or(a.state.status, GEMV_STATUS_GAVE_UP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (threadIdx.x == 0)
@@ -482,6 +477,7 @@ void gemv_kernel(GemvArgs a) {
     lds_barrier();
     const uint32_t epoch = uniform_late(epoch_v);
     float* cur = fused ? fused_planes(a, place.cz, epoch & 1u) : nullptr;
+    float* prev = fused ? fused_planes(a, place.cz, (epoch & 1u) ^ 1u) : nullptr;
     float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
     for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
         const int r = idx >> 7, n = idx & 127;
@@ -491,8 +487,11 @@ void gemv_kernel(GemvArgs a) {
         if (finisher) {
             red[r * 128 + n] = v;
         } else if (uint32_t(r) < a.rows) {
-            if (fused)
-                store_coherent(cur + (uint64_t(s) * a.rows + r) * 128u + n, v);
+            if (fused) {
+                const uint64_t word = (uint64_t(s) * a.rows + r) * 128u + n;
+                store_coherent(cur + word, v);
+                store_coherent(prev + word, __builtin_bit_cast(float, GEMV_PLANE_EMPTY));
+            }
             else
                 *(__attribute__((address_space(1))) float*)(plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c + n) = v;
         }
@@ -506,9 +505,7 @@ void gemv_kernel(GemvArgs a) {
         finish_columns(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
         return;
     }
-    finish_polled<(RT + GEMV_WAVES - 1) / GEMV_WAVES>(a, gw, op, y, c, red, cur,
-                                                       fused_planes(a, place.cz, (epoch & 1u) ^ 1u), epoch,
-                                                       place.cz);
+    finish_polled<(RT + GEMV_WAVES - 1) / GEMV_WAVES>(a, gw, op, y, c, red, cur, epoch, place.cz);
 }
 
 // ---------------------------------------------------------------------------
