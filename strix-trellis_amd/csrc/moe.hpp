@@ -26,6 +26,7 @@ struct MoeExpert {
 
 constexpr uint32_t MOE_MAX_ROUTES = 64;   // rows * k: one wave resolves all of them
 constexpr uint32_t MOE_MAX_TOPK = 8;
+constexpr uint32_t MOE_MAX_BANK = 256;       // experts a bank may hold
 
 struct MoeArgs {
     const MoeExpert* bank;

@@ -127,27 +127,32 @@ __device__ __forceinline__ MoeRoutes moe_routes(const MoeArgs& a) {
 // invalid tokens in order (there are at least as many: an invalid token's k
 // routes lead nothing).  One lane per route, in one wave (moe_group_shared).
 //
-// Groups are enumerated in leader order: each pass takes the lowest valid
-// route not yet grouped -- it leads its expert's group, since every lower
-// valid route belongs to an earlier group of another expert -- and removes the
-// whole group with one ballot.  Rank r stops after r + 1 passes.
-__device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank) {
+// A route leads its group when no lower valid route selects the same expert.
+// The leaders come from a table of each expert's first valid route (an LDS
+// minimum over the valid lanes), so the resolution costs the same for every
+// rank; the r-th leader in route order is the r-th set bit of their ballot.
+// `table` is MOE_MAX_BANK words of LDS that nothing else uses meanwhile.
+__device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank, uint32_t* table) {
     const int lane = threadIdx.x & 63;
     const uint32_t k = a.topk, n = a.rows * k;
     const bool live = uint32_t(lane) < n;
     const uint32_t slot = uint32_t(lane) % k;
     const MoeRoutes rt = moe_routes(a);
     const uint32_t id = rt.id;
-    const bool tv = (rt.valid >> lane) & 1;
-    const uint64_t valid = rt.valid, nonzero = rt.nonzero;
-    uint64_t rest = valid;
-    uint32_t groups = 0;
-    for (; rest; ++groups) {
-        const int lead = __builtin_ctzll(rest);
-        const uint32_t e = __builtin_amdgcn_readlane(id, lead);
-        const uint64_t members = __ballot(id == e) & valid;
-        if (groups == rank) return {members, members & nonzero, e, uint32_t(lead), true, -1};
-        rest &= ~members;
+    const bool tv = (rt.valid >> lane) & 1;   // valid implies id < bank_count <= MOE_MAX_BANK
+    for (uint32_t i = uint32_t(lane); i < a.bank_count; i += 64) table[i] = ~0u;
+    __builtin_amdgcn_wave_barrier();   // lanes exchange through the table: keep the three steps in order
+    if (tv) __hip_atomic_fetch_min(table + id, uint32_t(lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_wave_barrier();
+    const bool leads = tv && __hip_atomic_load(table + id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+                                 uint32_t(lane);
+    const uint64_t leaders = __ballot(leads);
+    const uint32_t groups = uint32_t(__builtin_popcountll(leaders));
+    if (rank < groups) {
+        const uint32_t lead = moe_nth_route(leaders, int(rank));
+        const uint32_t e = uint32_t(__builtin_amdgcn_readlane(int(id), int(lead)));
+        const uint64_t members = __ballot(id == e) & rt.valid;
+        return {members, members & rt.nonzero, e, lead, true, -1};
     }
     // Invalid tokens: slot 0 of each row whose routes are not valid.
     const uint64_t firsts = __ballot(live && slot == 0 && !tv);
@@ -189,11 +194,12 @@ __device__ __forceinline__ MoeGroup moe_uniform(const MoeGroup& g) {
 // The group of the workgroup (rank = grid z): wave 0 resolves it and shares
 // it through LDS (`slot`, 8 words), one barrier instead of four resolutions,
 // each a few hundred issue slots of a CU that the decode keeps busy.  With
-// `alone` (uniform) rank j is route j by itself (moe_resolve_route).
+// `alone` (uniform) rank j is route j by itself (moe_resolve_route).  `table`
+// (MOE_MAX_BANK words) is LDS that the workgroup uses only after the barrier.
 __device__ __forceinline__ MoeGroup moe_group_shared(const MoeArgs& a, uint32_t rank, uint32_t* slot,
-                                                     bool alone = false) {
+                                                     uint32_t* table, bool alone = false) {
     if (threadIdx.x < 64) {
-        const MoeGroup g = moe_uniform(alone ? moe_resolve_route(a, rank) : moe_resolve(a, rank));
+        const MoeGroup g = moe_uniform(alone ? moe_resolve_route(a, rank) : moe_resolve(a, rank, table));
         if (threadIdx.x == 0) {
             slot[0] = uint32_t(g.members);
             slot[1] = uint32_t(g.members >> 32);
@@ -272,6 +278,8 @@ constexpr int MOE_GU_ACT_BYTES = 2 * MOE_MAX_RT * MOE_GU_MAX_BPS * 16 * 2;
 constexpr int MOE_GU_RED_BYTES = GEMV_WAVES * 2 * MOE_MAX_RT * 128 * 4;
 constexpr int MOE_D_ACT_BYTES = MOE_MAX_RT * MOE_D_MAX_BPS * 16 * 2;
 constexpr int MOE_D_RED_BYTES = GEMV_WAVES * MOE_MAX_RT * 128 * 4;
+static_assert(MOE_GU_ACT_BYTES >= int(MOE_MAX_BANK * 4) && MOE_D_ACT_BYTES >= int(MOE_MAX_BANK * 4),
+              "the route resolution's expert table lives in the activation buffer");
 constexpr int moe_max(int a, int b) { return a > b ? a : b; }
 
 // Input-stage units of a wave (u = w, w + 4, ...) in batches of MOE_UNITS
@@ -405,7 +413,7 @@ void moe_gate_up_kernel(MoeArgs a) {
     __shared__ uint32_t group_slot[8];
     const uint32_t c = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot);
+    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot, reinterpret_cast<uint32_t*>(lds));
     if (!grp.leader || !grp.active) return;
     const uint32_t route = grp.route;
     const uint64_t active = grp.active;
@@ -611,7 +619,8 @@ void moe_down_kernel(MoeArgs a) {
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
     __shared__ uint32_t group_slot[8];
     const bool staged = a.down_mode != kMoeDownFused;   // a kernel argument: uniform
-    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot, a.down_mode == kMoeDownRouteCore);
+    const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot, reinterpret_cast<uint32_t*>(lds),
+                                          a.down_mode == kMoeDownRouteCore);
     if (!grp.leader) {
         // One workgroup per (invalid token, column group) writes its NaN row block.
         if (!staged && grp.nan_row >= 0 && split == 0 && tid < 128)
