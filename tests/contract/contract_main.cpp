@@ -601,6 +601,56 @@ static void moe_plan(strix_context c, hipStream_t hs) {
     CHECK(hipFree(split_ws) == hipSuccess);
     d.workspace = plain_ws;
     d.workspace_bytes = need;
+
+    // Device routes: bank ids are positions; the routes are device buffers.
+    // The workspace query of the extension matches the host-route queries.
+    std::vector<strix_tp_expert_desc> bank(ex);
+    for (uint32_t e = 0; e < experts; ++e) bank[e].expert_id = e;
+    auto* dev_ids = static_cast<uint32_t*>(device_alloc(rows * k * 4));
+    auto* dev_scores = static_cast<float*>(device_alloc(rows * k * 4));
+    strix_tp_moe_device_desc dd;
+    strix_tp_moe_device_desc_init(&dd);
+    dd.input = d.input;
+    dd.output = d.output;
+    dd.experts = bank.data();
+    dd.expert_count = experts;
+    dd.route_ids = dev_ids;
+    dd.route_ids_bytes = rows * k * 4;
+    dd.route_scores = dev_scores;
+    dd.route_scores_bytes = rows * k * 4;
+    uint64_t dev_plain = 0, dev_split = 0;
+    STATUS(strix_amd_tp_moe_device_workspace_bytes(c, &dd, 0, &dev_plain), STRIX_SUCCESS);
+    STATUS(strix_amd_tp_moe_device_workspace_bytes(c, &dd, 1, &dev_split), STRIX_SUCCESS);
+    CHECK(dev_plain == need && dev_split == split_need);
+    STATUS(strix_amd_tp_moe_device_workspace_bytes(c, &dd, 0, nullptr), STRIX_ERROR_INVALID_ARGUMENT);
+    bank[1].expert_id = 7;   // not its position
+    STATUS(strix_amd_tp_moe_device_workspace_bytes(c, &dd, 1, &dev_split), STRIX_ERROR_INVALID_ARGUMENT);
+    CHECK(dev_split == 0);
+    bank[1].expert_id = 1;
+    dd.route_scores_bytes = rows * k * 4 - 4;   // routes of both kinds must match
+    STATUS(strix_tp_moe_plan_create_device_split(c, &dd, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+    dd.route_scores_bytes = rows * k * 4;
+    void* dev_ws = device_alloc(split_need);
+    dd.workspace = dev_ws;
+    dd.workspace_bytes = need;   // enough for a plain plan only
+    STATUS(strix_tp_moe_plan_create_device_split(c, &dd, &st, &p), STRIX_ERROR_INSUFFICIENT_BUFFER);
+    const size_t live2 = fake::live.size();
+    STATUS(strix_tp_moe_plan_create_device(c, &dd, &st, &p), STRIX_SUCCESS);
+    STATUS(strix_tp_moe_plan_down_core(p), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_tp_moe_plan_destroy(p), STRIX_SUCCESS);
+    dd.workspace_bytes = split_need;
+    STATUS(strix_tp_moe_plan_create_device_split(c, &dd, &st, &p), STRIX_SUCCESS);
+    fake::launches.clear();
+    STATUS(strix_tp_moe_plan_submit(p), STRIX_SUCCESS);
+    STATUS(strix_tp_moe_plan_down_core(p), STRIX_SUCCESS);
+    STATUS(strix_tp_moe_plan_down_reference_core(p), STRIX_SUCCESS);
+    STATUS(strix_tp_moe_plan_down_finish(p), STRIX_SUCCESS);
+    CHECK(fake::launches.size() == 5 && fake::launches[3].name == "moe_down_route_core" &&
+          fake::launches[4].name == "moe_down_finish");
+    STATUS(strix_tp_moe_plan_destroy(p), STRIX_SUCCESS);
+    CHECK(fake::live.size() == live2);
+    for (void* q : {static_cast<void*>(dev_ids), static_cast<void*>(dev_scores), dev_ws}) CHECK(hipFree(q) == hipSuccess);
+
     for (strix_weights w : ws) STATUS(strix_weights_destroy(w), STRIX_SUCCESS);
     for (void* q : {x, y, d.workspace}) CHECK(hipFree(q) == hipSuccess);
 }
