@@ -44,9 +44,12 @@ hipError_t launch_moe_down_core(const MoeArgs& a, MoeDownMode mode, hipStream_t 
 __global__ __launch_bounds__(64) void moe_down_finish_kernel(MoeArgs a) {
     const uint32_t c = blockIdx.x, r = blockIdx.y;
     const int lane = threadIdx.x;
+    __shared__ uint32_t route_words[2 * MOE_MAX_ROUTES];
     const MoeRoutes rt = moe_routes(a);
+    moe_keep_routes(rt, route_words);
+    __builtin_amdgcn_wave_barrier();
     if ((rt.valid >> (r * a.topk)) & 1) {
-        moe_finish_token(a, r, c, lane);
+        moe_finish_token(a, r, c, lane, route_words);
     } else {
         float* yr = a.y + uint64_t(r) * a.y_stride + 128 * c;
         yr[lane] = yr[lane + 64] = __builtin_bit_cast(float, 0x7fc00000u);

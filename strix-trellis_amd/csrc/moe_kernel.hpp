@@ -96,6 +96,7 @@ struct MoeGroup {
 // the bank and distinct from its other ids, and each score is finite and >= 0.
 struct MoeRoutes {
     uint32_t id;
+    float score;
     uint64_t valid, nonzero;
 };
 __device__ __forceinline__ MoeRoutes moe_routes(const MoeArgs& a) {
@@ -115,7 +116,16 @@ __device__ __forceinline__ MoeRoutes moe_routes(const MoeArgs& a) {
     const uint64_t bad = __ballot(live && !ok);
     const uint64_t row_bits = live ? ((1ull << k) - 1) << (row * k) : 0;   // k <= 8, row*k + k <= 64
     const bool tv = live && (bad & row_bits) == 0;
-    return {id, __ballot(tv), __ballot(live && sc != 0.0f)};
+    return {id, sc, __ballot(tv), __ballot(live && sc != 0.0f)};
+}
+
+// Every route's bank index and score (word j and MOE_MAX_ROUTES + j of
+// `words`, LDS), written by the wave that resolved them, so that a later
+// token finish in the same workgroup reads them without a memory round trip.
+__device__ __forceinline__ void moe_keep_routes(const MoeRoutes& rt, uint32_t* words) {
+    const int lane = threadIdx.x & 63;
+    words[lane] = rt.id;
+    words[MOE_MAX_ROUTES + lane] = __builtin_bit_cast(uint32_t, rt.score);
 }
 
 // Workgroup rank r (grid z, the slowest dimension) takes the r-th expert group
@@ -132,12 +142,14 @@ __device__ __forceinline__ MoeRoutes moe_routes(const MoeArgs& a) {
 // minimum over the valid lanes), so the resolution costs the same for every
 // rank; the r-th leader in route order is the r-th set bit of their ballot.
 // `table` is MOE_MAX_BANK words of LDS that nothing else uses meanwhile.
-__device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank, uint32_t* table) {
+__device__ __forceinline__ MoeGroup moe_resolve(const MoeArgs& a, uint32_t rank, uint32_t* table,
+                                                uint32_t* keep = nullptr) {
     const int lane = threadIdx.x & 63;
     const uint32_t k = a.topk, n = a.rows * k;
     const bool live = uint32_t(lane) < n;
     const uint32_t slot = uint32_t(lane) % k;
     const MoeRoutes rt = moe_routes(a);
+    if (keep) moe_keep_routes(rt, keep);
     const uint32_t id = rt.id;
     const bool tv = (rt.valid >> lane) & 1;   // valid implies id < bank_count <= MOE_MAX_BANK
     for (uint32_t i = uint32_t(lane); i < a.bank_count; i += 64) table[i] = ~0u;
@@ -195,11 +207,13 @@ __device__ __forceinline__ MoeGroup moe_uniform(const MoeGroup& g) {
 // it through LDS (`slot`, 8 words), one barrier instead of four resolutions,
 // each a few hundred issue slots of a CU that the decode keeps busy.  With
 // `alone` (uniform) rank j is route j by itself (moe_resolve_route).  `table`
-// (MOE_MAX_BANK words) is LDS that the workgroup uses only after the barrier.
+// (MOE_MAX_BANK words) is LDS that the workgroup uses only after the barrier;
+// `keep` (2 x MOE_MAX_ROUTES words of LDS, or null) receives every route's bank
+// index and score (moe_keep_routes).
 __device__ __forceinline__ MoeGroup moe_group_shared(const MoeArgs& a, uint32_t rank, uint32_t* slot,
-                                                     uint32_t* table, bool alone = false) {
+                                                     uint32_t* table, bool alone = false, uint32_t* keep = nullptr) {
     if (threadIdx.x < 64) {
-        const MoeGroup g = moe_uniform(alone ? moe_resolve_route(a, rank) : moe_resolve(a, rank, table));
+        const MoeGroup g = moe_uniform(alone ? moe_resolve_route(a, rank) : moe_resolve(a, rank, table, keep));
         if (threadIdx.x == 0) {
             slot[0] = uint32_t(g.members);
             slot[1] = uint32_t(g.members >> 32);
@@ -538,13 +552,15 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
 // planes of every slot are loaded together, so a token waits for about three
 // memory round trips however many slots it has.  A zero-score slot loads
 // nothing of its expert and adds no term.  Used by the fused down's last
-// arrival and by the staged finish, so both give the same bits.
-__device__ __forceinline__ void moe_finish_token(const MoeArgs& a, uint32_t r, uint32_t c, int lane) {
+// arrival and by the staged finish, so both give the same bits.  `routes` is
+// every route's bank index and score in LDS (moe_keep_routes).
+__device__ __forceinline__ void moe_finish_token(const MoeArgs& a, uint32_t r, uint32_t c, int lane,
+                                                 const uint32_t* routes) {
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
     const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
     const uint32_t jl = r * k + (uint32_t(lane) < k ? uint32_t(lane) : 0u);
-    const float sc_l = ld_global(a.scores + jl);
-    const MoeExpert& el = a.bank[ld_global(a.ids + jl)];
+    const float sc_l = __builtin_bit_cast(float, routes[MOE_MAX_ROUTES + jl]);
+    const MoeExpert& el = a.bank[routes[jl]];
     const uint64_t svh_l = reinterpret_cast<uintptr_t>(el.down.svh);
     const uint64_t bias_l = reinterpret_cast<uintptr_t>(el.down.bias);
     float sc[MOE_MAX_TOPK], z0[MOE_MAX_TOPK], z1[MOE_MAX_TOPK], b0[MOE_MAX_TOPK], b1[MOE_MAX_TOPK];
@@ -619,8 +635,9 @@ void moe_down_kernel(MoeArgs a) {
     const uint32_t k = a.topk, I = a.I, S = a.s_d;
     __shared__ uint32_t group_slot[8];
     const bool staged = a.down_mode != kMoeDownFused;   // a kernel argument: uniform
+    __shared__ uint32_t route_words[2 * MOE_MAX_ROUTES];
     const MoeGroup grp = moe_group_shared(a, blockIdx.z, group_slot, reinterpret_cast<uint32_t*>(lds),
-                                          a.down_mode == kMoeDownRouteCore);
+                                          a.down_mode == kMoeDownRouteCore, route_words);
     if (!grp.leader) {
         // One workgroup per (invalid token, column group) writes its NaN row block.
         if (!staged && grp.nan_row >= 0 && split == 0 && tid < 128)
@@ -672,7 +689,7 @@ void moe_down_kernel(MoeArgs a) {
     for (uint32_t m = fm; m; m &= m - 1, ++q) {
         if (q % GEMV_WAVES != w) continue;
         const uint32_t r = uint32_t(__builtin_ctz(m));
-        moe_finish_token(a, r, c, lane);
+        moe_finish_token(a, r, c, lane, route_words);
         if (lane == 0) __hip_atomic_store(a.c_d + uint64_t(r) * (I >> 7) + c, 0u, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
     }
