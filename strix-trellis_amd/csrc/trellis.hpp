@@ -119,7 +119,10 @@ __device__ __forceinline__ void link_chunk(Chunk<K>& c, bool first_of_tile) {
 // Its 16 bits end (8V+F+1)*K bits after the chunk start.  Returns a register
 // whose low (HI = false) or high (HI = true) 16 bits are the state; the other
 // half is don't-care, because every consumer reads 16-bit operands.  Two
-// windows 16 bits apart share one v_alignbit (K = 2, 4, 8).
+// windows 16 bits apart share one v_alignbit (K = 2, 4, 8).  Other widths have
+// no such pairs, so their windows take the high half only where it is a word's
+// own high half (no v_alignbit); a v_pk_* product of a high half counts as a
+// high-half write for the compiler, whose next reader then waits a state.
 // ---------------------------------------------------------------------------
 template <int K, int V, int F>
 struct Window {
@@ -127,7 +130,7 @@ struct Window {
     static constexpr int shift = 32 * K - end;   // distance of the window LSB from the chunk LSB
     static constexpr int q = shift / 32;
     static constexpr int r = shift % 32;
-    static constexpr bool hi = r >= 16;
+    static constexpr bool hi = r == 16 || (r > 16 && 16 % K == 0);
     static constexpr int align = hi ? r - 16 : r;
 
     __device__ __forceinline__ static uint32_t reg(const Chunk<K>& c) {
