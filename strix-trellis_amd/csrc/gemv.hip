@@ -20,7 +20,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_finish_kernel(GemvArgs a) {
     const GroupWeights gw = group_weights(a, z);
     float* y = a.y + z * a.y_group_stride;
     const float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
-    finish_columns(a, gw, column_operands(gw, c), y, c, a.splits, [&](int s, int r) -> const float* {
+    finish_columns(a, gw, column_operands(gw, c, a.N), y, c, a.splits, [&](int s, int r) -> const float* {
         return plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c;
     });
 }
@@ -36,7 +36,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void plane_finish_kernel(GemvArgs a) 
     const int c = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const uint32_t r0 = (blockIdx.y * GEMV_WAVES + w) * kPlaneRowsPerWave;
     if (r0 >= a.rows) return;
-    const ColumnOperands op = column_operands(a.w, c);
+    const ColumnOperands op = column_operands(a.w, c, a.N);
     constexpr int P = int(kPlaneRowsPerWave);
     float z0[P], z1[P];
 #pragma unroll

@@ -87,14 +87,19 @@ struct ColumnOperands {
     float b0, b1;
 };
 
-__device__ __forceinline__ ColumnOperands column_operands(const GroupWeights& gw, int c) {
-    const int lane = threadIdx.x & 63;
-    const int n0 = 128 * c + lane, n1 = n0 + 64;
+// A missing bias is read through an empty buffer range (zeros, no memory
+// access) rather than behind a branch: with every load unconditional the
+// compiler counts outstanding loads exactly, and the plane polls issued next
+// do not wait for these operands to arrive first.
+__device__ __forceinline__ ColumnOperands column_operands(const GroupWeights& gw, int c, uint32_t N) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t n0 = 128u * c + lane, n1 = n0 + 64;
     ColumnOperands o;
     o.sv0 = ld_global(gw.svh + n0);
     o.sv1 = ld_global(gw.svh + n1);
-    o.b0 = gw.bias ? ld_global(gw.bias + n0) : 0.0f;
-    o.b1 = gw.bias ? ld_global(gw.bias + n1) : 0.0f;
+    const auto rb = make_rsrc(gw.bias, gw.bias ? N * 4u : 0u);
+    o.b0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, n0 * 4u, 0, 0));
+    o.b1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, n1 * 4u, 0, 0));
     return o;
 }
 
@@ -499,7 +504,7 @@ void gemv_kernel(GemvArgs a) {
     if (!finisher) return;
     // Loading the output-stage operands in the prologue instead keeps them
     // live across the main loop and made the 1-row kernel spill (slower).
-    const ColumnOperands op = column_operands(gw, c);
+    const ColumnOperands op = column_operands(gw, c, a.N);
     lds_barrier();
     if (a.splits == 1) {
         finish_columns(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
@@ -622,7 +627,7 @@ __global__ __launch_bounds__(OWNER_THREADS) void gemv_owner_kernel(GemvArgs a) {
     __syncthreads();
     const int wv = tid >> 6;
     if (wv < RT && uint32_t(wv) < a.rows) {
-        const ColumnOperands op = column_operands(gw, int(c));
+        const ColumnOperands op = column_operands(gw, int(c), a.N);
         float z0 = rows[wv * 128 + lane], z1 = rows[wv * 128 + lane + 64];
         h32_wave(z0, z1);
         const int n0 = 128 * int(c) + lane, n1 = n0 + 64;
