@@ -39,6 +39,7 @@ namespace stx {
 
 constexpr int GEMV_WAVES = 4;
 constexpr int GEMV_THREADS = 64 * GEMV_WAVES;
+constexpr uint32_t kGemvCus = 256;   // compute units of an MI355X (8 XCDs x 32)
 
 struct GemvArgs {
     GroupWeights w;               // weights of a single-group launch
@@ -443,6 +444,15 @@ void gemv_kernel(GemvArgs a) {
     InputLoad pre[kUnits];
     batch_load(w, pre);
     __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the weight prefetch
+    // A grid of two dispatch rounds (257..512 workgroups on 256 CUs, the
+    // 4096^2 decode shape): each CU's vector loads return in issue order, so
+    // the second workgroup's input would wait behind the first one's weight
+    // ring.  The first round's workgroups therefore issue their ring only once
+    // their own input has arrived (4096^2 K4 R1: 7.56 -> 7.45 us).  With three
+    // or more rounds the same wait measured 1-3 % slower, so it is not taken.
+    if (gridDim.x <= 2 * kGemvCus && blockIdx.x + kGemvCus < gridDim.x)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
     Chunk<K> ring[4];
 #pragma unroll
