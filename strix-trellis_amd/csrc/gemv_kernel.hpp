@@ -447,16 +447,21 @@ void gemv_kernel(GemvArgs a) {
     // A grid of two dispatch rounds (257..512 workgroups on 256 CUs, the
     // 4096^2 decode shape): each CU's vector loads return in issue order, so
     // the second workgroup's input would wait behind the first one's weight
-    // ring.  The first round's workgroups therefore issue their ring only once
-    // their own input has arrived (4096^2 K4 R1: 7.56 -> 7.45 us).  With three
-    // or more rounds the same wait measured 1-3 % slower, so it is not taken.
-    if (gridDim.x <= 2 * kGemvCus && blockIdx.x + kGemvCus < gridDim.x)
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-
+    // ring.  The first round's workgroups therefore issue one block of the
+    // ring, then the rest only once their own input has arrived (4096^2 K4 R1:
+    // 7.53 -> 7.32 us; the whole ring after the input: 7.46 us).  With three or
+    // more rounds the wait measured 1-3 % slower, so it is not taken.
     Chunk<K> ring[4];
+    load_chunk(ring[0], rsrc, block_off(0));
+    __builtin_amdgcn_sched_barrier(0);
+    if (gridDim.x <= 2 * kGemvCus && blockIdx.x + kGemvCus < gridDim.x) {
+        // every load but block 0's (one instruction for K <= 4, two above)
+        if constexpr (K <= 4) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) load_chunk(ring[u], rsrc, block_off(u));
+    for (int u = 1; u < 4; ++u) load_chunk(ring[u], rsrc, block_off(u));
 
     // The chunks stay in their registers across the input stage: decoding
     // blocks ahead of the barrier (to overlap the input loads) was measured
