@@ -76,9 +76,15 @@ strix_status strix_amd_set_gemm_handoff(strix_context context, uint32_t always_t
 /* Single-launch GEMV plans (linear plans with rows 1-8, grouped plans, TP
  * dense plans): the workgroup of each output group's last input split waits,
  * with a bounded poll, for the other splits' published partial sums.  A wait
- * that runs out writes NaN outputs and sets STRIX_AMD_GEMV_GAVE_UP in the
- * plan's sticky status word; later submissions of the plan stay correct
- * (partials carry a per-launch tag, so a late one is never folded).
+ * that runs out writes NaN outputs, sets STRIX_AMD_GEMV_GAVE_UP in the plan's
+ * sticky status word and poisons that output group: workgroups are dispatched
+ * in order only within one XCD, so a split of the given-up launch may start
+ * after the give-up and publish into the planes the next launch reads.  So
+ * every later submission writes NaN to the poisoned output groups until
+ * strix_amd_plan_status / strix_amd_grouped_plan_status with clear != 0
+ * re-initialises the plan's state (in stream order, after every earlier
+ * launch has ended).  TP dense plans have no status call: a give-up there
+ * shows as NaN outputs, and the plan is recreated.
  * poll_limit = rounds of that wait for every later submission on the context
  * (a round is a few hundred ns); 0 makes every finisher give up at once (test
  * hook).  strix_amd_set_gemv_poll_limit(context, STRIX_AMD_GEMV_POLL_DEFAULT)
@@ -88,10 +94,24 @@ strix_status strix_amd_set_gemm_handoff(strix_context context, uint32_t always_t
 strix_status strix_amd_set_gemv_poll_limit(strix_context context, uint32_t poll_limit);
 
 /* Sticky status flags of a single-launch plan (0 for plans that need no
- * wait), read after synchronising the plan's stream; clear != 0 also resets
- * them (enqueued before the synchronisation). */
+ * wait), read after synchronising the plan's stream; clear != 0 also
+ * re-initialises the plan's whole single-launch state (status, launch epochs
+ * and partial planes; enqueued before the synchronisation), which lifts a
+ * give-up's poison.  The caller orders it after every submission and graph
+ * replay of the plan it must follow. */
 strix_status strix_amd_plan_status(strix_linear_plan plan, uint32_t clear, uint32_t *flags);
 strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan plan, uint32_t clear, uint32_t *flags);
+
+/* Single-launch state of destroyed linear and TP dense plans.  By default,
+ * as the reference keeps its plans' completion counters, the state of every
+ * plan lives until its weights are destroyed and distinct plans never share
+ * state, so graphs captured from a destroyed plan may still replay at any
+ * time.  enable != 0 lets plans created later on the context take an idle
+ * state block of a destroyed plan on the same weights (re-initialised on the
+ * new plan's stream), which bounds the state held by the plans alive at one
+ * time; the caller then must not replay a destroyed plan's graphs after
+ * creating a new plan on those weights. */
+strix_status strix_amd_set_plan_state_reuse(strix_context context, uint32_t enable);
 
 /* Measured call floor: one kernel of `workgroups` x 256 threads reads `bytes`
  * device bytes from src once (16-byte loads, the decode GEMV's load depth) and

@@ -110,12 +110,19 @@ strix_status strix_amd_set_gemv_poll_limit(strix_context c, uint32_t poll_limit)
     return device;
 }
 
+strix_status strix_amd_set_plan_state_reuse(strix_context c, uint32_t enable) {
+    const strix_status device = on_context_device(c);
+    if (device == STRIX_SUCCESS) c->reuse_plan_state = enable != 0;
+    return device;
+}
+
 strix_status strix_amd_plan_status(strix_linear_plan p, uint32_t clear, uint32_t* flags) {
     if (flags) *flags = 0;
     if (!p || !flags) return STRIX_ERROR_INVALID_ARGUMENT;
     const strix_status device = on_context_device(p->owner);
     if (device != STRIX_SUCCESS) return device;
-    return read_fused_status(p->fused, p->stream, flags, clear);
+    return read_fused_status(p->fused, p->block.bytes, stx::fused_planes_offset(p->weights->dev, 1), p->stream, flags,
+                             clear);
 }
 
 strix_status strix_amd_stream_read(strix_context c, const void* src, uint64_t bytes, uint32_t workgroups,

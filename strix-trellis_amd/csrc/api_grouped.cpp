@@ -9,7 +9,7 @@
 // strix_gemv (STRIX_GEMV_ROW_INVARIANT_R1).  Workspace layout, all offsets a
 // function of the geometry only:
 //   [group table: kMaxGroups entries][single-launch state of G groups]
-// (the state's status word, launch epochs and tagged planes: backend.hpp).
+// (the state's status word, launch epochs and partial planes: backend.hpp).
 // The workspace is dedicated to the plan: creation uploads the table,
 // initialises the state and synchronises the stream; one launch per submission.
 #include "api_internal.hpp"
@@ -96,6 +96,7 @@ struct strix_grouped_gemv_plan_impl {
     stx::LinearCall call{};
     const stx::GroupWeights* table = nullptr;
     stx::FusedState fused{};   // null when one split suffices
+    uint64_t state_bytes = 0;  // bytes of that state
     bool owner = false;        // owner-fold plan (no planes) instead of the split plan
     uint64_t xgs = 0, ygs = 0;
     hipStream_t stream{};
@@ -174,8 +175,10 @@ strix_status strix_grouped_gemv_plan_create(strix_context c, const strix_grouped
     p->call.alpha = 1.0f;
     p->call.beta = 0.0f;
     p->call.workspace = nullptr;
-    if (v.layout.state_bytes)
+    if (v.layout.state_bytes) {
         p->fused = stx::fused_state_at(base + v.layout.state_offset, v.geometry, v.rows, uint32_t(v.weights.size()));
+        p->state_bytes = v.layout.state_bytes;
+    }
     const uint32_t G = uint32_t(v.weights.size());
     const bool want_owner = c->grouped_fold == 2 ||
                             (c->grouped_fold == 0 && stx::grouped_owner_preferred(v.geometry, G, v.rows));
@@ -206,7 +209,8 @@ strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan p, uint32_t c
     if (!p || !flags) return STRIX_ERROR_INVALID_ARGUMENT;
     const strix_status s = on_context_device(p->owner_ctx);
     if (s != STRIX_SUCCESS) return s;
-    return read_fused_status(p->fused, p->stream, flags, clear);
+    return read_fused_status(p->fused, p->state_bytes, stx::fused_planes_offset(p->geometry, uint32_t(p->retained.size())),
+                             p->stream, flags, clear);
 }
 
 strix_status strix_amd_grouped_plan_fold(strix_grouped_gemv_plan p, uint32_t* fold) {

@@ -26,6 +26,7 @@ struct strix_context_impl {
     uint32_t gemv_poll_limit = stx::GEMV_DEFAULT_POLL_LIMIT;   // single-launch GEMV finishers
     void* gemv_scratch = nullptr;   // this device's static scratch (strix_amd_gemv_noalloc)
     uint32_t grouped_fold = 0;      // grouped plans created on it: 0 library's choice, 1 split, 2 owner
+    bool reuse_plan_state = false;  // plans created on it may take a destroyed plan's single-launch state
 };
 
 struct strix_weights_impl {
@@ -36,11 +37,14 @@ struct strix_weights_impl {
     uint64_t plans = 0;       // live plans retaining these weights
     // Single-launch state (planes, epochs, status) of plans created on these
     // weights.  Graphs captured from a plan may replay after the plan is
-    // destroyed, so the arrays live until the weights are destroyed.
+    // destroyed, so the arrays live until the weights are destroyed, and
+    // distinct plans never share one (the reference's rule for its completion
+    // counters).
     std::vector<void*> counter_arrays;
-    // Blocks of counter_arrays whose plans were destroyed: a later plan that
-    // needs a block of the same size re-initialises and takes one, so the
-    // state held stays bounded by the plans alive at one time.
+    // Blocks of counter_arrays whose plans were destroyed.  Only on a context
+    // that opted in (strix_amd_set_plan_state_reuse) does a later plan that
+    // needs a block of the same size re-initialise and take one; the state
+    // held then stays bounded by the plans alive at one time.
     std::vector<std::pair<void*, uint64_t>> idle_states;
 };
 
@@ -157,8 +161,11 @@ strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, st
                               FusedBlock& block);
 // A destroyed plan's block becomes idle (it stays allocated with the weights).
 void release_fused_state(strix_weights w, FusedBlock& block);
-// Sticky status word of a single-launch state: read (synchronising `hs`) and
-// optionally cleared.
-strix_status read_fused_status(const stx::FusedState& st, hipStream_t hs, uint32_t* flags, uint32_t clear);
+// Sticky status word of a single-launch state of `bytes` (planes from
+// `planes_offset`): read (synchronising `hs`); with `clear` the whole state
+// is re-initialised on `hs` first (status and epochs 0, every plane EMPTY),
+// which also lifts a give-up's poison.
+strix_status read_fused_status(const stx::FusedState& st, uint64_t bytes, uint64_t planes_offset, hipStream_t hs,
+                               uint32_t* flags, uint32_t clear);
 
 }  // namespace stx_api

@@ -31,7 +31,7 @@ strix_status make_fused_state(strix_weights w, uint64_t rows, hipStream_t hs, st
     if (!bytes) return STRIX_SUCCESS;
     void* state = nullptr;
     bool reused = false;
-    for (auto it = w->idle_states.begin(); it != w->idle_states.end(); ++it) {
+    for (auto it = w->idle_states.begin(); w->owner->reuse_plan_state && it != w->idle_states.end(); ++it) {
         if (it->second == bytes) {
             state = it->first;
             w->idle_states.erase(it);
@@ -72,12 +72,13 @@ void release_fused_state(strix_weights w, FusedBlock& block) {
     block = {};
 }
 
-strix_status read_fused_status(const stx::FusedState& st, hipStream_t hs, uint32_t* flags, uint32_t clear) {
+strix_status read_fused_status(const stx::FusedState& st, uint64_t bytes, uint64_t planes_offset, hipStream_t hs,
+                               uint32_t* flags, uint32_t clear) {
     *flags = 0;
     if (!st.status) return STRIX_SUCCESS;
     uint32_t word = 0;
     hipError_t e = hipMemcpyAsync(&word, st.status, sizeof(word), hipMemcpyDeviceToHost, hs);
-    if (e == hipSuccess && clear) e = stx::launch_fill_u32(st.status, 0u, 1, hs);
+    if (e == hipSuccess && clear) e = init_fused_state(st.status, bytes, planes_offset, hs);
     if (e == hipSuccess) e = hipStreamSynchronize(hs);
     if (e != hipSuccess) return status_of(e);
     *flags = word;

@@ -24,6 +24,7 @@
 
 #include <cmath>
 #include <new>
+#include <type_traits>
 #include <unordered_map>
 
 using namespace stx_api;
@@ -206,9 +207,13 @@ strix_status device_check(strix_context c, const strix_tp_moe_device_desc* d, Mo
         if (d->experts[i].expert_id != i) return STRIX_ERROR_INVALID_ARGUMENT;
     if ((s = device_resident(c, Span(d->route_ids, d->route_ids_bytes), 4)) != STRIX_SUCCESS) return s;
     if ((s = device_resident(c, Span(d->route_scores, d->route_scores_bytes), 4)) != STRIX_SUCCESS) return s;
-    if (Span(d->route_ids, d->route_ids_bytes).meets(Span(d->route_scores, d->route_scores_bytes)) ||
-        Span(d->route_ids, d->route_ids_bytes).meets(Span(d->output.data, v.y_bytes)) ||
-        Span(d->route_scores, d->route_scores_bytes).meets(Span(d->output.data, v.y_bytes)))
+    // Pairwise disjoint with the input and the output (the workspace is
+    // checked with the others in create_plan), as the reference requires of
+    // all five buffers (src/tp_api.inc:407-416): the kernels write hidden, P
+    // and Y while later workgroups still read the routes.
+    const Span ids(d->route_ids, d->route_ids_bytes), scores(d->route_scores, d->route_scores_bytes);
+    const Span x(d->input.data, v.x_bytes), y(d->output.data, v.y_bytes);
+    if (ids.meets(scores) || ids.meets(y) || scores.meets(y) || ids.meets(x) || scores.meets(x))
         return STRIX_ERROR_INVALID_ARGUMENT;
     v.args.ids = d->route_ids;
     v.args.scores = d->route_scores;
@@ -228,6 +233,11 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
         return STRIX_ERROR_INVALID_ARGUMENT;
     for (strix_weights w : v.retained)
         if (touches(d->workspace, d->workspace_bytes, w)) return STRIX_ERROR_INVALID_ARGUMENT;
+    if constexpr (std::is_same_v<D, strix_tp_moe_device_desc>) {
+        const Span ws(d->workspace, d->workspace_bytes);
+        if (ws.meets(Span(d->route_ids, d->route_ids_bytes)) || ws.meets(Span(d->route_scores, d->route_scores_bytes)))
+            return STRIX_ERROR_INVALID_ARGUMENT;
+    }
     if ((s = device_resident(c, Span(d->input.data, v.x_bytes), 4)) != STRIX_SUCCESS) return s;
     if ((s = device_resident(c, Span(d->output.data, v.y_bytes), 4)) != STRIX_SUCCESS) return s;
     if ((s = device_resident(c, Span(d->workspace, d->workspace_bytes), kWorkspaceAlign)) != STRIX_SUCCESS) return s;

@@ -52,9 +52,11 @@ uint64_t linear_workspace_bytes(const DeviceWeights& w, uint64_t rows);
 // its plane there and re-arms (EMPTY-fills) its plane of the other set, which
 // the previous launch used and which nothing of this launch reads; the
 // finisher polls set e & 1 until no word is EMPTY, then advances epochs[g].
-// A partial published late (after a finisher gave up, before its launch
-// ended) lands in a set the next launch does not read, and whose planes that
-// launch's splits re-arm.
+// A finisher that gives up sets GEMV_EPOCH_POISON in epochs[g] instead: a
+// split of that launch that starts only after the give-up cannot be told
+// apart from the next launch's splits, so no later finisher of g trusts a
+// plane (each writes NaN) until the host re-initialises the whole state
+// (init_fused_state) in stream order.
 struct FusedState {
     uint32_t* status = nullptr;
     uint32_t* epochs = nullptr;
@@ -62,6 +64,7 @@ struct FusedState {
 };
 constexpr uint32_t GEMV_PLANE_EMPTY = 0xFFFFFFFFu;
 constexpr uint32_t GEMV_STATUS_GAVE_UP = 1u;
+constexpr uint32_t GEMV_EPOCH_POISON = 0x80000000u;
 // Poll rounds before a finisher gives up (a few hundred ms); 0 gives up at
 // once without polling (test hook).
 constexpr uint32_t GEMV_DEFAULT_POLL_LIMIT = 1u << 22;
@@ -90,7 +93,7 @@ struct LinearCall {
 // Generic GEMV (rows 1..8): core kernel + finishing kernel, no counters.
 hipError_t launch_gemv(const DeviceWeights& w, const LinearCall& call, hipStream_t stream);
 // Single-launch GEMV: the workgroup of the last split of each 128-output group
-// waits for the other splits' tagged planes and finishes (state as above).
+// waits for the other splits' published planes and finishes (state as above).
 hipError_t launch_gemv_fused(const DeviceWeights& w, const LinearCall& call, const FusedState& state,
                              hipStream_t stream);
 // Second launch of a split-K core: folds planes[S][rows][N] (row stride N) in

@@ -116,7 +116,7 @@ static GemvLaunch make_launch(const DeviceWeights& w, const GroupWeights* table,
 
 // The per-split buffer resource spans bps rows of tiles and must stay below
 // 2^31 bytes (its out-of-range sentinel); the 1-D grid holds every column
-// group x split; the tagged planes of one column group fit a buffer resource.
+// group x split; the planes of one column group fit a buffer resource.
 static bool gemv_fits(const DeviceWeights& w, uint32_t groups, uint64_t rows) {
     const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
     const uint64_t cgs = uint64_t(w.output / 128) * groups;

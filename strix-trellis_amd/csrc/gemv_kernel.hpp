@@ -159,12 +159,19 @@ __device__ __forceinline__ void finish_columns(const GemvArgs& a, const GroupWei
 //     carry 13 zero low bits, and EMPTY has none.
 //   * Publication and polls are device-scope accesses (sc1): a store is
 //     written through to memory, a poll reads past the L1.
-//   * The poll is bounded: a finisher that gives up writes NaN outputs, sets
-//     GEMV_STATUS_GAVE_UP in the sticky status word and still advances the
-//     epoch; partials that land afterwards (before this launch ends) sit in a
-//     set the next launch does not read, and its splits re-arm that set.
-//   * Its dependencies were dispatched before it and at most ncg * groups
-//     finishers exist, so the wait always ends.
+//   * The poll is bounded.  A finisher that gives up writes NaN outputs, sets
+//     GEMV_STATUS_GAVE_UP in the sticky status word and poisons epochs[cz]
+//     (GEMV_EPOCH_POISON).  Workgroups are dispatched in grid order only
+//     within one XCD, so a split of the same launch may still start after the
+//     give-up: it reads the epoch as the next launch's splits will, and no
+//     word of the state tells the two apart.  Instead a finisher that reads a
+//     poisoned epoch trusts no plane: it writes NaN without polling, and the
+//     column group stays poisoned until the host re-initialises the whole
+//     state in stream order (after every earlier launch, late splits
+//     included, has ended).
+//   * Its dependencies were dispatched before it on their XCDs and at most
+//     ncg * groups finishers exist, so the wait ends unless another stream's
+//     work holds CUs for longer than the poll limit.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t load_epoch(const uint32_t* p) {
     return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -191,91 +198,186 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// `own` holds this workgroup's [rows][128] sums (split S-1); `cur` the
-// column group's planes of this launch's set.
-// Wave w takes rows w, w+4 (RPW = 1 or 2 rows per wave): the loads of both
-// rows are issued in one poll round (kFoldBatch / RPW splits per round).
-template <int RPW>
-__device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeights& gw, const ColumnOperands& op,
-                                              float* y, int c, const float* own, const float* cur,
-                                              uint32_t epoch, uint32_t cz) {
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int others = int(a.splits) - 1;
-    constexpr int B = kFoldBatch / RPW;
-    bool gave_up = false;
-    if (uint32_t(w) < a.rows) {
-        uint32_t rr[RPW];
-        bool live[RPW];
+// Plane poll: the F32 words of columns 2l and 2l + 1 at voffset + soffset of
+// the planes, one 64-bit device-coherent load (sc1, the cache policy of an
+// agent-scope atomic load).  Each 32-bit word is seen whole or not at all;
+// the two words are checked separately.
+constexpr int kCoherentAux = 16;   // sc1
+typedef float gemv_f2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ gemv_f2_t poll_pair(__amdgpu_buffer_rsrc_t planes, uint32_t voffset, uint32_t soffset) {
+    return __builtin_bit_cast(gemv_f2_t,
+                              __builtin_amdgcn_raw_buffer_load_b64(planes, voffset, soffset, kCoherentAux));
+}
+__device__ __forceinline__ bool filled(gemv_f2_t v) {
+    return __builtin_bit_cast(uint32_t, v.x) != GEMV_PLANE_EMPTY && __builtin_bit_cast(uint32_t, v.y) != GEMV_PLANE_EMPTY;
+}
+
+// The plane stride, opaque to the compiler: the poll offsets derived from it
+// are recomputed (one scalar add each) in every poll round instead of being
+// hoisted out of the loop, where every live offset would hold a scalar
+// register.
+__device__ __forceinline__ uint32_t step_offset(uint32_t bytes) {
+    asm volatile("" : "+s"(bytes));
+    return bytes;
+}
+
+// 64-bit plane loads one lane holds in flight in one poll round (a wave's
+// vector-load counter tracks at most 63).
+constexpr int kPollLoads = 32;
+constexpr uint32_t kPollOutOfRange = 0x80000000u;   // answered with zeros (filled), never folded
+
+// One poll round of P x NB pair loads per lane: load (p, u) at soffset
+// (first + u) * stride + p * row_step, for p < rows_live and u < count (both
+// wave-uniform; the rest out of range, so every load is issued before the
+// first wait and none sits behind a branch).  Polls until every word has
+// arrived or the limit runs out (false); then adds load u to z[p] for
+// u < count in ascending u.
+template <int P, int NB>
+__device__ __forceinline__ bool poll_fold_round(gemv_f2_t (&z)[P], __amdgpu_buffer_rsrc_t planes, uint32_t voff,
+                                                uint32_t first, uint32_t stride, uint32_t row_step, int rows_live,
+                                                int count, uint32_t limit) {
+    gemv_f2_t v[P][NB];
+    for (uint32_t spin = 0;; ++spin) {
+        asm volatile("" ::: "memory");
+        const int cnt = int(step_offset(uint32_t(count)));
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            rr[i] = uint32_t(w + GEMV_WAVES * i);
-            live[i] = rr[i] < a.rows;
-            if (!live[i]) rr[i] = uint32_t(w);   // a valid row again, result unused
-        }
-        float z0[RPW], z1[RPW];
+        for (int p = 0; p < P; ++p) {
+            uint32_t so = step_offset(stride) * first + uint32_t(p) * row_step;
+            const int c = p < rows_live ? cnt : 0;
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) z0[i] = z1[i] = 0.0f;
-        bool complete = a.poll_limit != 0;
-        for (int s = 0; s < others && complete; s += B) {
-            float v0[RPW][B], v1[RPW][B];
-            for (uint32_t spin = 0;; ++spin) {
-#pragma unroll
-                for (int i = 0; i < RPW; ++i)
-#pragma unroll
-                    for (int u = 0; u < B; ++u) {
-                        const float* p = cur + ((s + u < others ? s + u : others - 1) * a.rows + rr[i]) * 128u;
-                        v0[i][u] = load_coherent(p + lane);
-                        v1[i][u] = load_coherent(p + lane + 64);
-                    }
-                bool ready = true;
-#pragma unroll
-                for (int i = 0; i < RPW; ++i)
-#pragma unroll
-                    for (int u = 0; u < B; ++u)
-                        ready = ready && (s + u >= others ||
-                                          (__builtin_bit_cast(uint32_t, v0[i][u]) != GEMV_PLANE_EMPTY &&
-                                           __builtin_bit_cast(uint32_t, v1[i][u]) != GEMV_PLANE_EMPTY));
-                if (__all(ready)) break;
-                if (spin + 1 >= a.poll_limit) {
-                    complete = false;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
+            for (int u = 0; u < NB; ++u) {
+                v[p][u] = poll_pair(planes, u < c ? voff : kPollOutOfRange, so);
+                so += stride;
             }
+        }
+        bool ready = true;
 #pragma unroll
-            for (int i = 0; i < RPW; ++i)
+        for (int p = 0; p < P; ++p)
 #pragma unroll
-                for (int u = 0; u < B; ++u) {
-                    if (s + u < others) {
-                        z0[i] = z0[i] + v0[i][u];
-                        z1[i] = z1[i] + v1[i][u];
-                    }
-                }
+            for (int u = 0; u < NB; ++u) ready &= filled(v[p][u]);
+        if (__all(ready)) break;
+        if (spin + 1 >= limit) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const float t0 = z[p].x + v[p][u].x, t1 = z[p].y + v[p][u].y;
+            z[p].x = u < count ? t0 : z[p].x;
+            z[p].y = u < count ? t1 : z[p].y;
+        }
+    return true;
+}
+
+// H32 of P rows held as element pairs (2l, 2l + 1) per lane: the stride-1
+// level inside the lane, strides 2..64 across lanes 1..32 apart.  Each level
+// combines the same element pairs with the same operations (lower + upper,
+// lower - upper, one FP32 rounding each) as h32_wave, so the bits are those
+// of h32_wave on the (l, l + 64) layout.
+template <int P>
+__device__ __forceinline__ void h32_pairs(gemv_f2_t (&v)[P]) {
+    float v0[P], v1[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const float a = v[i].x, b = v[i].y;
+        v0[i] = a + b;
+        v1[i] = a - b;
+    }
+    auto stage = [&](auto st) {
+        constexpr int S = decltype(st)::value;
+#pragma unroll
+        for (int i = 0; i < P; ++i) butterfly<S>(v0[i], v1[i]);
+    };
+    stage(std::integral_constant<int, 1>{});
+    stage(std::integral_constant<int, 2>{});
+    stage(std::integral_constant<int, 4>{});
+    stage(std::integral_constant<int, 8>{});
+    stage(std::integral_constant<int, 16>{});
+    stage(std::integral_constant<int, 32>{});
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        v[i].x = rn32(v0[i] * INV_SQRT128);
+        v[i].y = rn32(v1[i] * INV_SQRT128);
+    }
+}
+
+// Finisher of a single launch.  `red` holds this workgroup's [rows][128] sums
+// (split S-1); `flag` is an LDS word cleared before the barrier that precedes
+// this call; `cur` the column group's planes of this launch's set.  Wave w
+// finishes rows w and w + 4, lane l columns 2l and 2l + 1 of them: it loads
+// each other split's word pair with one 64-bit load, kPollLoads per round
+// over its rows (one round for up to 32 other splits at rows <= 4, 16 at
+// five to eight), folds ((+0 + P0) + P1) + ... + P(S-2) + own -- the split
+// fold of the two-launch path, bit for bit -- and applies H32 and the output
+// stage.  Each wave polls with its own bound; a wave that gives up writes
+// NaN rows, and after a barrier the workgroup poisons the epoch if any did.
+template <int RT>
+__device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeights& gw, float* y, int c,
+                                              const float* red, uint32_t* flag, const float* cur, uint32_t epoch,
+                                              uint32_t cz) {
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    constexpr int RPW = (RT + GEMV_WAVES - 1) / GEMV_WAVES, B = kPollLoads / RPW;
+    if (uint32_t(w) < a.rows) {
+        const int others = int(a.splits) - 1;
+        const uint32_t stride = a.rows * 512u;   // one split's [rows][128] F32
+        const auto planes = make_rsrc(cur, uint32_t(others) * stride);
+        const uint32_t limit = a.poll_limit, voff = uint32_t(w) * 512u + uint32_t(lane) * 8u;
+        const int rows_live = uint32_t(w + GEMV_WAVES) < a.rows && RPW > 1 ? 2 : 1;
+        // Output-stage operands of columns 128c + 2l, +1 (in flight during the polls).
+        const uint32_t n0 = 128u * uint32_t(c) + 2u * uint32_t(lane);
+        const uint32_t svp = ld_global(reinterpret_cast<const uint32_t*>(gw.svh + n0));
+        const auto rb = make_rsrc(gw.bias, gw.bias ? a.N * 4u : 0u);
+        const gemv_f2_t bias = __builtin_bit_cast(gemv_f2_t, __builtin_amdgcn_raw_buffer_load_b64(rb, n0 * 4u, 0, 0));
+        gemv_f2_t z[RPW];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) z[i] = gemv_f2_t{0.0f, 0.0f};
+        bool complete = limit != 0 && !(epoch & GEMV_EPOCH_POISON);
+        for (int s0 = 0; s0 < others && complete;) {
+            const int count = others - s0 < B ? others - s0 : B;
+            constexpr uint32_t step = GEMV_WAVES * 512u;
+            if (count <= 8)
+                complete = poll_fold_round<RPW, 8>(z, planes, voff, uint32_t(s0), stride, step, rows_live, count, limit);
+            else if (count <= 16 || B <= 16)
+                complete = poll_fold_round<RPW, (B < 16 ? B : 16)>(z, planes, voff, uint32_t(s0), stride, step,
+                                                                   rows_live, count, limit);
+            else if (count <= 24)
+                complete = poll_fold_round<RPW, 24>(z, planes, voff, uint32_t(s0), stride, step, rows_live, count,
+                                                    limit);
+            else
+                complete = poll_fold_round<RPW, B>(z, planes, voff, uint32_t(s0), stride, step, rows_live, count, limit);
+            s0 += count;
         }
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
-            z0[i] = z0[i] + own[rr[i] * 128 + lane];
-            z1[i] = z1[i] + own[rr[i] * 128 + lane + 64];
-            if (!complete) z0[i] = z1[i] = __builtin_nanf("");
+            const uint32_t r = uint32_t(w + GEMV_WAVES * i) < a.rows ? uint32_t(w + GEMV_WAVES * i) : uint32_t(w);
+            const gemv_f2_t own = *reinterpret_cast<const gemv_f2_t*>(red + r * 128 + 2 * lane);
+            z[i].x = complete ? z[i].x + own.x : __builtin_nanf("");
+            z[i].y = complete ? z[i].y + own.y : __builtin_nanf("");
         }
-        gave_up = !complete;
-        h32_wave_multi<RPW>(z0, z1);
-        const int n0 = 128 * c + lane, n1 = n0 + 64;
+        if (!complete) *flag = 1u;
+        h32_pairs<RPW>(z);
+        const uint16_t sv0 = uint16_t(svp), sv1 = uint16_t(svp >> 16);
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
-            if (!live[i]) continue;
-            float* yr = y + rr[i] * a.y_row_stride;
-            const float o0 = output_value(z0[i], op.sv0, gw.bias != nullptr, op.b0, a.alpha, a.beta, yr + n0);
-            const float o1 = output_value(z1[i], op.sv1, gw.bias != nullptr, op.b1, a.alpha, a.beta, yr + n1);
-            *(__attribute__((address_space(1))) float*)(yr + n0) = o0;
-            *(__attribute__((address_space(1))) float*)(yr + n1) = o1;
+            if (i >= rows_live) continue;
+            float* yr = y + uint32_t(w + GEMV_WAVES * i) * a.y_row_stride + n0;
+            gemv_f2_t o;
+            o.x = output_value(z[i].x, sv0, gw.bias != nullptr, bias.x, a.alpha, a.beta, yr);
+            o.y = output_value(z[i].y, sv1, gw.bias != nullptr, bias.y, a.alpha, a.beta, yr + 1);
+            *(__attribute__((address_space(1))) gemv_f2_t*)(yr) = o;
         }
     }
-    // Advance the epoch (the splits have re-armed the other set).
-    if (gave_up && lane == 0)
-        __hip_atomic_fetch_or(a.state.status, GEMV_STATUS_GAVE_UP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0)
-        __hip_atomic_store(a.state.epochs + cz, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Every wave's verdict is in `flag`: advance the epoch (the splits have
+    // re-armed the other set), or poison it.  Off the outputs' critical path.
+    lds_barrier();
+    if (threadIdx.x == 0) {
+        const bool gave_up = *flag != 0u;
+        if (gave_up)
+            __hip_atomic_fetch_or(a.state.status, GEMV_STATUS_GAVE_UP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t next = gave_up ? (epoch | GEMV_EPOCH_POISON) : ((epoch + 1u) & ~GEMV_EPOCH_POISON);
+        __hip_atomic_store(a.state.epochs + cz, next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -361,10 +463,10 @@ __device__ __forceinline__ void mfma_partials(const MfmaAcc<RT>& acc, float* red
 
 // Register budget: five waves per SIMD (<= 96 VGPRs), measured faster than
 // four (C1 8.9 -> 8.3 us; 16 x 4096 -> 1024 R4 32.5 -> 30.4 us) even where the
-// grid is smaller than one resident round.  The 8-row K >= 6 instances would
-// spill at that budget and keep four.
+// grid is smaller than one resident round.  The 8-row K >= 6 and 6-row K8
+// instances would spill at that budget and keep four.
 template <int K, int RT>
-constexpr int gemv_waves_per_eu() { return RT == 8 && K >= 6 ? 4 : 5; }
+constexpr int gemv_waves_per_eu() { return (RT == 8 && K >= 6) || (RT == 6 && K == 8) ? 4 : 5; }
 
 template <int K, int CB, int RT>
 __global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu<K, RT>())))
@@ -517,15 +619,20 @@ void gemv_kernel(GemvArgs a) {
         }
     }
     if (!finisher) return;
-    // Loading the output-stage operands in the prologue instead keeps them
-    // live across the main loop and made the 1-row kernel spill (slower).
-    const ColumnOperands op = column_operands(gw, c, a.N);
-    lds_barrier();
+    // The core inputs are dead (every wave has passed the barrier after its
+    // loop): their first word is the finisher's give-up flag.
+    uint32_t* flag = reinterpret_cast<uint32_t*>(smem);
+    if (tid == 0) *flag = 0u;
     if (a.splits == 1) {
+        // Loading the output-stage operands in the prologue instead keeps them
+        // live across the main loop and made the 1-row kernel spill (slower).
+        const ColumnOperands op = column_operands(gw, c, a.N);
+        lds_barrier();
         finish_columns(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
         return;
     }
-    finish_polled<(RT + GEMV_WAVES - 1) / GEMV_WAVES>(a, gw, op, y, c, red, cur, epoch, place.cz);
+    lds_barrier();
+    finish_polled<RT>(a, gw, y, c, red, flag, cur, epoch, place.cz);
 }
 
 // ---------------------------------------------------------------------------

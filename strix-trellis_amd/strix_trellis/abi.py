@@ -189,6 +189,7 @@ _PROTOTYPES = {
     "strix_amd_tp_moe_device_workspace_bytes": (_S, [vp, C.POINTER(TpMoeDeviceDesc), u32, C.POINTER(u64)]),
     "strix_amd_set_gemm_handoff": (_S, [vp, u32]),
     "strix_amd_set_gemv_poll_limit": (_S, [vp, u32]),
+    "strix_amd_set_plan_state_reuse": (_S, [vp, u32]),
     "strix_amd_plan_status": (_S, [vp, u32, C.POINTER(u32)]),
     "strix_amd_grouped_plan_status": (_S, [vp, u32, C.POINTER(u32)]),
     "strix_amd_stream_read": (_S, [vp, vp, u64, u32, vp, C.POINTER(Stream)]),

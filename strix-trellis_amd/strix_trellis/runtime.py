@@ -66,6 +66,11 @@ class Context:
         """Poll rounds of single-launch GEMV finishers on later submissions (0: give up at once)."""
         abi.check(self.lib.strix_amd_set_gemv_poll_limit(self.handle, int(limit)), "strix_amd_set_gemv_poll_limit")
 
+    def set_plan_state_reuse(self, enable=True):
+        """Let plans created later take a destroyed plan's single-launch state (off by default)."""
+        abi.check(self.lib.strix_amd_set_plan_state_reuse(self.handle, int(bool(enable))),
+                  "strix_amd_set_plan_state_reuse")
+
     def set_grouped_fold(self, fold=abi.FOLD_AUTO):
         """Fold of grouped plans created later: FOLD_AUTO, FOLD_SPLIT or FOLD_OWNER."""
         abi.check(self.lib.strix_amd_set_grouped_fold(self.handle, int(fold)), "strix_amd_set_grouped_fold")
@@ -301,7 +306,10 @@ class LinearPlan:
         return n.value
 
     def status(self, clear=False):
-        """Sticky status flags of a single-launch plan (abi.GEMV_GAVE_UP); synchronises its stream."""
+        """Sticky status flags of a single-launch plan (abi.GEMV_GAVE_UP); synchronises its stream.
+
+        clear=True re-initialises the plan's whole single-launch state (status,
+        epochs, planes), which lifts the poison a give-up leaves."""
         f = C.c_uint32()
         abi.check(self.lib.strix_amd_plan_status(self.handle, int(bool(clear)), C.byref(f)), "strix_amd_plan_status")
         return f.value

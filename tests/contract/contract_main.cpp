@@ -421,17 +421,44 @@ static void direct_calls(strix_context c, hipStream_t hs) {
     fake::reset_failures();
     STATUS(strix_linear_plan_create(c, &m, &st, 7, &bad), STRIX_ERROR_INVALID_ARGUMENT);
 
-    // Create/destroy cycles: a destroyed plan's planes become idle and the
-    // next plan of the same size takes them, initialised again (two fills)
-    // with no allocation, so the state held stays bounded.
+    // By default (the reference's rule) every plan gets a state of its own,
+    // held with the weights until they are destroyed, so graphs captured from
+    // a destroyed plan never share it with a later plan.
     m = matmul(d, 4, 2);
-    const size_t live2 = fake::live.size();
+    const size_t live_before = fake::live.size();
+    for (int cycle = 0; cycle < 3; ++cycle) {
+        const fake::Counters c0 = fake::n;
+        strix_linear_plan tp = nullptr;
+        STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &tp), STRIX_SUCCESS);
+        CHECK(fake::n.mallocs == c0.mallocs + 1);
+        CHECK(fake::live.size() == live_before + size_t(cycle) + 1);
+        STATUS(strix_linear_plan_destroy(tp), STRIX_SUCCESS);
+    }
+    // Clearing a plan's status re-initialises its whole state (two fills:
+    // status and epochs, then the planes) before the synchronisation.
+    {
+        fake::launches.clear();
+        const fake::Counters c0 = fake::n;
+        uint32_t flags = 7;
+        STATUS(strix_amd_plan_status(gp, 1, &flags), STRIX_SUCCESS);
+        CHECK(flags == 0 && fake::n.syncs == c0.syncs + 1 && fake::n.mallocs == c0.mallocs);
+        CHECK(fake::launches.size() == 2 && fake::launches[0].name == "fill" && fake::launches[1].name == "fill");
+        fake::launches.clear();
+        STATUS(strix_amd_plan_status(gp, 0, &flags), STRIX_SUCCESS);
+        CHECK(fake::launches.empty());
+    }
+
+    // With reuse enabled, a destroyed plan's planes become idle and the next
+    // plan of the same size takes them, initialised again (two fills) with no
+    // allocation, so the state held stays bounded.
+    STATUS(strix_amd_set_plan_state_reuse(c, 1), STRIX_SUCCESS);
+    const size_t live2 = fake::live.size() - 1;   // one idle block of this size is there to take
     for (int cycle = 0; cycle < 4; ++cycle) {
         fake::launches.clear();
         const fake::Counters c0 = fake::n;
         strix_linear_plan tp = nullptr;
         STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &tp), STRIX_SUCCESS);
-        CHECK(fake::n.mallocs == c0.mallocs + (cycle == 0 ? 1 : 0));   // gp still holds the first block
+        CHECK(fake::n.mallocs == c0.mallocs);   // an idle block of the default-mode cycles
         CHECK(fake::live.size() == live2 + 1);
         CHECK(fake::launches.size() == 2 && fake::launches[0].name == "fill" && fake::launches[1].name == "fill");
         STATUS(strix_linear_plan_destroy(tp), STRIX_SUCCESS);
@@ -447,6 +474,7 @@ static void direct_calls(strix_context c, hipStream_t hs) {
     STATUS(strix_linear_plan_create(c, &m, &st, STRIX_OPERATION_GEMV, &again), STRIX_SUCCESS);
     CHECK(fake::n.mallocs == c1.mallocs && fake::live.size() == live2 + 1);
     STATUS(strix_linear_plan_destroy(again), STRIX_SUCCESS);
+    STATUS(strix_amd_set_plan_state_reuse(c, 0), STRIX_SUCCESS);
 
     // Weights outlive their plans; the planes go with the weights.
     STATUS(strix_weights_destroy(d.w), STRIX_ERROR_INVALID_ARGUMENT);
@@ -639,6 +667,27 @@ static void moe_plan(strix_context c, hipStream_t hs) {
     STATUS(strix_tp_moe_plan_down_core(p), STRIX_ERROR_INVALID_ARGUMENT);
     STATUS(strix_tp_moe_plan_destroy(p), STRIX_SUCCESS);
     dd.workspace_bytes = split_need;
+    // The routes must not meet the input, the output or the workspace (hidden
+    // or P), as the reference requires of all five buffers; nothing is left
+    // allocated by a rejected creation.
+    {
+        const size_t live3 = fake::live.size();
+        char* wsb = static_cast<char*>(dev_ws);
+        dd.route_ids = reinterpret_cast<uint32_t*>(wsb);   // inside hidden
+        STATUS(strix_tp_moe_plan_create_device_split(c, &dd, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+        STATUS(strix_tp_moe_plan_create_device(c, &dd, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+        dd.route_ids = dev_ids;
+        dd.route_scores = reinterpret_cast<float*>(wsb + split_need - rows * k * 4);   // inside P
+        STATUS(strix_tp_moe_plan_create_device_split(c, &dd, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+        dd.route_scores = dev_scores;
+        dd.route_ids = static_cast<uint32_t*>(const_cast<void*>(dd.input.data));   // over the input
+        STATUS(strix_tp_moe_plan_create_device_split(c, &dd, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+        dd.route_ids = dev_ids;
+        dd.route_scores = static_cast<float*>(dd.output.data);   // over the output
+        STATUS(strix_tp_moe_plan_create_device(c, &dd, &st, &p), STRIX_ERROR_INVALID_ARGUMENT);
+        dd.route_scores = dev_scores;
+        CHECK(fake::live.size() == live3);
+    }
     STATUS(strix_tp_moe_plan_create_device_split(c, &dd, &st, &p), STRIX_SUCCESS);
     fake::launches.clear();
     STATUS(strix_tp_moe_plan_submit(p), STRIX_SUCCESS);

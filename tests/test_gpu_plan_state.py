@@ -1,19 +1,26 @@
-"""Single-launch GEMV plans: tagged planes, launch epochs and the sticky give-up state.
+"""Single-launch GEMV plans: published planes, launch epochs and the sticky, poisoning give-up.
 
-A single-launch plan's finisher waits (bounded) for the other splits' tagged
+A single-launch plan's finisher waits (bounded) for the other splits' published
 partials.  These tests force the give-up path from the host
 (strix_amd_set_gemv_poll_limit(ctx, 0): every finisher gives up at once, so
 every kernel still exits normally) and check that
 
   * the give-up is reported: NaN outputs and STRIX_AMD_GEMV_GAVE_UP in the
-    plan's sticky status, which stays set until cleared;
-  * the next submission with the default limit returns the exact bits of the
-    two-launch strix_gemv, although the given-up launch's partials landed in
-    the planes after its finisher left (their tag is stale);
+    plan's sticky status word;
+  * it poisons the plan: later submissions with the default limit write NaN
+    again (no plane is trusted, since a split of the given-up launch may have
+    started after the give-up and published into the next launch's planes),
+    and the flag stays set;
+  * clearing the status re-initialises the state: the next submissions return
+    the exact bits of the two-launch strix_gemv;
   * many submissions in a row, with inputs rewritten between them, each carry
     the bits of strix_gemv (the epoch advances every launch);
-  * a plan created after another was destroyed takes over its planes,
-    initialised again.
+  * a plan created after another was destroyed starts clean, whether it takes
+    a fresh state (the default) or the destroyed plan's (opt-in reuse).
+
+The interleavings a forced give-up cannot produce on the GPU (a split that
+starts after its finisher gave up) are covered by the CPU model in
+tests/test_gemv_protocol.py.
 
 Also the call-floor kernel (strix_amd_stream_read): every workgroup's XOR of
 its slice of the source.
@@ -72,13 +79,19 @@ def test_linear_plan_give_up_then_exact(ctx, R):
         assert plan.status() == abi.GEMV_GAVE_UP
 
         ctx.set_gemv_poll_limit(abi.GEMV_POLL_DEFAULT)
+        for rep in range(2):
+            y.fill_(0.0)
+            plan.submit()
+            torch.cuda.synchronize()
+            assert torch.isnan(y).all(), f"submission {rep} after the give-up trusts a poisoned plane set"
+        assert plan.status() == abi.GEMV_GAVE_UP, "the status is sticky"
+        assert plan.status(clear=True) == abi.GEMV_GAVE_UP
+        assert plan.status() == 0
         for rep in range(3):
             y.fill_(0.0)
             plan.submit()
             torch.cuda.synchronize()
-            np.testing.assert_array_equal(_bits(y), _bits(ref), err_msg=f"submission {rep} after the give-up")
-        assert plan.status() == abi.GEMV_GAVE_UP, "the status is sticky"
-        assert plan.status(clear=True) == abi.GEMV_GAVE_UP
+            np.testing.assert_array_equal(_bits(y), _bits(ref), err_msg=f"submission {rep} after the clear")
         assert plan.status() == 0
     finally:
         ctx.set_gemv_poll_limit(abi.GEMV_POLL_DEFAULT)
@@ -138,9 +151,13 @@ def test_grouped_plan_give_up_then_exact(ctx):
         y.fill_(0.0)
         plan.submit()
         torch.cuda.synchronize()
-        np.testing.assert_array_equal(_bits(y), _bits(ref))
+        assert torch.isnan(y).all(), "a poisoned grouped plan trusts no plane until cleared"
         assert plan.status(clear=True) == abi.GEMV_GAVE_UP
         assert plan.status() == 0
+        y.fill_(0.0)
+        plan.submit()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_bits(y), _bits(ref))
     finally:
         ctx.set_gemv_poll_limit(abi.GEMV_POLL_DEFAULT)
         plan.destroy()
@@ -148,18 +165,22 @@ def test_grouped_plan_give_up_then_exact(ctx):
             w.destroy()
 
 
-def test_plan_state_reused_after_destroy(ctx):
-    # A destroyed plan's planes go idle and the next plan of the same rows on
-    # the same weights takes them, initialised again: the new plan neither
-    # inherits the old one's sticky give-up nor folds its stale partials.
+@pytest.mark.parametrize("reuse", [False, True])
+def test_plan_after_destroy_starts_clean(ctx, reuse):
+    # A plan created after a poisoned plan on the same weights was destroyed
+    # starts clean: by default with a state of its own (the destroyed plan's
+    # stays allocated with the weights), with reuse enabled with the destroyed
+    # plan's block, initialised again.  Either way it neither inherits the
+    # sticky give-up nor folds stale partials.
     I, N, K, R = 4096, 4096, 4, 2
-    print(f"plan state reuse {I}x{N} K{K} R{R}", flush=True)
+    print(f"plan after destroy {I}x{N} K{K} R{R} reuse={reuse}", flush=True)
     tr, suh, svh, _ = synth.layer(I, N, K, synth.BASE_SEED + 90)
     w = runtime.Weights(ctx, tr, suh, svh, None, "mul1")
     x = torch.from_numpy(synth.activations(R, I, synth.BASE_SEED + 91)).to(DEV)
     y = torch.empty((R, N), device=DEV)
     ref = torch.empty((R, N), device=DEV)
     runtime.gemv(w, x, ref)
+    ctx.set_plan_state_reuse(reuse)
     first = runtime.LinearPlan(w, x, y)
     second = None
     try:
@@ -180,6 +201,7 @@ def test_plan_state_reused_after_destroy(ctx):
         assert second.status() == 0
     finally:
         ctx.set_gemv_poll_limit(abi.GEMV_POLL_DEFAULT)
+        ctx.set_plan_state_reuse(False)
         for plan in (first, second):
             if plan is not None:
                 plan.destroy()
