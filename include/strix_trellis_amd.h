@@ -113,10 +113,16 @@ strix_status strix_amd_grouped_plan_status(strix_grouped_gemv_plan plan, uint32_
  * creating a new plan on those weights. */
 strix_status strix_amd_set_plan_state_reuse(strix_context context, uint32_t enable);
 
-/* Measured call floor: one kernel of `workgroups` x 256 threads reads `bytes`
- * device bytes from src once (16-byte loads, the decode GEMV's load depth) and
- * stores one word per workgroup into sink.  bytes must be a multiple of
- * 16 * workgroups; nothing else is read or written. */
+/* Streaming read, the measurement kernel of the read ceiling and the call
+ * floors: one kernel of `workgroups` x `threads` threads reads `bytes` device
+ * bytes from src once, each workgroup a contiguous slice, each lane keeping
+ * `depth` 16-byte loads in flight, and stores the XOR of each workgroup's
+ * slice (one word per workgroup) into sink.  threads is 64, 128, 256, 512 or
+ * 1024; depth is 1, 2, 4, 8 or 16; bytes must be a multiple of
+ * 16 * workgroups; nothing else is read or written.  strix_amd_stream_read is
+ * the 256-thread, depth-4 shape (the decode GEMV's load depth). */
+strix_status strix_amd_stream_read_shaped(strix_context context, const void *src, uint64_t bytes,
+    uint32_t workgroups, uint32_t threads, uint32_t depth, uint32_t *sink, const strix_stream *stream);
 strix_status strix_amd_stream_read(strix_context context, const void *src, uint64_t bytes, uint32_t workgroups,
     uint32_t *sink, const strix_stream *stream);
 

@@ -125,18 +125,25 @@ strix_status strix_amd_plan_status(strix_linear_plan p, uint32_t clear, uint32_t
                              clear);
 }
 
-strix_status strix_amd_stream_read(strix_context c, const void* src, uint64_t bytes, uint32_t workgroups,
-                                   uint32_t* sink, const strix_stream* stream) {
+strix_status strix_amd_stream_read_shaped(strix_context c, const void* src, uint64_t bytes, uint32_t workgroups,
+                                          uint32_t threads, uint32_t depth, uint32_t* sink,
+                                          const strix_stream* stream) {
     hipStream_t hs{};
     Rules r;
     r.then([&] { return on_context_device(c); })
         .then([&] { return borrowed_stream(c, stream, hs); })
-        .need(workgroups && bytes && bytes % (16ull * workgroups) == 0 && bytes / workgroups < (uint64_t(1) << 31),
+        .need(workgroups && bytes && bytes % (16ull * workgroups) == 0 && bytes / workgroups < (uint64_t(1) << 31) &&
+                  stx::stream_read_shape_ok(threads, depth),
               STRIX_ERROR_INVALID_ARGUMENT)
         .then([&] { return device_resident(c, Span(src, bytes), 16); })
         .then([&] { return device_resident(c, Span(sink, uint64_t(workgroups) * 4), 4); })
-        .then([&] { return status_of(stx::launch_stream_read(src, bytes, workgroups, sink, hs)); });
+        .then([&] { return status_of(stx::launch_stream_read(src, bytes, workgroups, threads, depth, sink, hs)); });
     return r.status();
+}
+
+strix_status strix_amd_stream_read(strix_context c, const void* src, uint64_t bytes, uint32_t workgroups,
+                                   uint32_t* sink, const strix_stream* stream) {
+    return strix_amd_stream_read_shaped(c, src, bytes, workgroups, 256, 4, sink, stream);
 }
 
 }  // extern "C"

@@ -141,10 +141,13 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t count, hipStrea
 constexpr uint64_t kGemvScratchBytes = uint64_t(4) << 20;
 hipError_t gemv_scratch_address(int device, void** out);
 
-// Streaming read of `bytes` (a multiple of 16) by `workgroups` x 256 threads,
-// 16-byte loads, nothing stored but one word per workgroup into sink: the
-// measured call floor of a kernel that reads that many bytes once.
-hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* sink,
-                              hipStream_t stream);
+// Streaming read of `bytes` (a multiple of 16 * workgroups) by `workgroups` x
+// `threads` threads (64..1024, a power of two), `depth` (1..16, a power of
+// two) 16-byte loads in flight per lane, nothing stored but one word per
+// workgroup into sink: the read ceiling and the call floor of a kernel that
+// reads that many bytes once are the fastest such shapes.
+bool stream_read_shape_ok(uint32_t threads, uint32_t depth);
+hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t threads, uint32_t depth,
+                              uint32_t* sink, hipStream_t stream);
 
 }  // namespace stx

@@ -248,37 +248,66 @@ hipError_t launch_output_stage(const DeviceWeights& w, const float* core, uint64
 }
 
 // Streaming read: workgroup b reads its contiguous 1/workgroups of the bytes
-// with 16-byte buffer loads, up to four per lane in flight (the decode GEMV's
-// prefetch depth), and folds them with XOR; one word per workgroup is stored.
-__global__ __launch_bounds__(256) void stream_read_kernel(const unsigned char* src, uint64_t bytes,
-                                                          uint32_t* sink) {
+// with 16-byte buffer loads and folds them with XOR; one word per workgroup is
+// stored.  Each lane keeps DEPTH loads in flight as a rolling ring (a load is
+// refilled as soon as its slot is consumed), so the read never drains between
+// batches; loads past the slice are out of range (zeros, no memory access).
+// The call floor of a kernel that reads a given number of bytes once is the
+// fastest of these shapes (threads x depth x workgroups).
+template <int DEPTH, int THREADS>
+__global__ __launch_bounds__(THREADS) void stream_read_kernel(const unsigned char* src, uint64_t bytes,
+                                                              uint32_t* sink) {
     const uint64_t per = bytes / gridDim.x;   // a multiple of 16 (checked by the launcher)
     const auto rsrc = make_rsrc(src + uint64_t(blockIdx.x) * per, uint32_t(per));
-    const uint32_t n = uint32_t(per / 16);
+    const uint32_t n = uint32_t(per / 16), loads = (n + THREADS - 1) / THREADS;
+    auto off = [&](uint32_t t) -> uint32_t {
+        const uint32_t j = threadIdx.x + t * THREADS;
+        return j < n ? j * 16u : 0x80000000u;
+    };
+    u32x4 ring[DEPTH];
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) ring[u] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off(u), 0, 0);
     u32x4 acc = {0u, 0u, 0u, 0u};
-    for (uint32_t i = threadIdx.x; i < n; i += 4 * 256) {
-        u32x4 v[4];
+    for (uint32_t t = 0; t < loads; t += DEPTH) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t j = i + u * 256;
-            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, j < n ? j * 16u : 0x80000000u, 0, 0);
+        for (int u = 0; u < DEPTH; ++u) {
+            acc ^= ring[u];
+            ring[u] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off(t + u + DEPTH), 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc ^= v[u];
     }
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) acc ^= ring[u];   // out of range: zeros
     uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
-    for (int off = 32; off > 0; off >>= 1) r ^= __shfl_xor(r, off);
-    __shared__ uint32_t part[4];
+    for (int off2 = 32; off2 > 0; off2 >>= 1) r ^= __shfl_xor(r, off2);
+    __shared__ uint32_t part[THREADS / 64];
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = r;
     __syncthreads();
-    if (threadIdx.x == 0) sink[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+    if (threadIdx.x == 0) {
+        uint32_t v = 0;
+        for (int k = 0; k < THREADS / 64; ++k) v ^= part[k];
+        sink[blockIdx.x] = v;
+    }
 }
 
-hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* sink,
-                              hipStream_t stream) {
-    if (!workgroups || bytes % (16ull * workgroups) || bytes / workgroups >= (uint64_t(1) << 31))
+hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t threads, uint32_t depth,
+                              uint32_t* sink, hipStream_t stream) {
+    if (!workgroups || bytes % (16ull * workgroups) || bytes / workgroups >= (uint64_t(1) << 31) ||
+        !stream_read_shape_ok(threads, depth))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(stream_read_kernel, dim3(workgroups), dim3(256), 0, stream,
+    using Fn = void (*)(const unsigned char*, uint64_t, uint32_t*);
+    static const Fn table[5][5] = {
+        {stream_read_kernel<1, 64>, stream_read_kernel<2, 64>, stream_read_kernel<4, 64>, stream_read_kernel<8, 64>,
+         stream_read_kernel<16, 64>},
+        {stream_read_kernel<1, 128>, stream_read_kernel<2, 128>, stream_read_kernel<4, 128>,
+         stream_read_kernel<8, 128>, stream_read_kernel<16, 128>},
+        {stream_read_kernel<1, 256>, stream_read_kernel<2, 256>, stream_read_kernel<4, 256>,
+         stream_read_kernel<8, 256>, stream_read_kernel<16, 256>},
+        {stream_read_kernel<1, 512>, stream_read_kernel<2, 512>, stream_read_kernel<4, 512>,
+         stream_read_kernel<8, 512>, stream_read_kernel<16, 512>},
+        {stream_read_kernel<1, 1024>, stream_read_kernel<2, 1024>, stream_read_kernel<4, 1024>,
+         stream_read_kernel<8, 1024>, stream_read_kernel<16, 1024>}};
+    const int ti = __builtin_ctz(threads) - 6, di = __builtin_ctz(depth);
+    hipLaunchKernelGGL(table[ti][di], dim3(workgroups), dim3(threads), 0, stream,
                        static_cast<const unsigned char*>(src), bytes, sink);
     return hipGetLastError();
 }

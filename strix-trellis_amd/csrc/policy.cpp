@@ -222,4 +222,12 @@ uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t 
     return uint64_t(routes) * (H / 128) + uint64_t(rows) * (I / 128);
 }
 
+// Shapes of the streaming-read kernel (launch_stream_read): the kernel is
+// instantiated for these thread counts and loads in flight per lane.
+bool stream_read_shape_ok(uint32_t threads, uint32_t depth) {
+    const bool t = threads == 64 || threads == 128 || threads == 256 || threads == 512 || threads == 1024;
+    const bool d = depth == 1 || depth == 2 || depth == 4 || depth == 8 || depth == 16;
+    return t && d;
+}
+
 }  // namespace stx

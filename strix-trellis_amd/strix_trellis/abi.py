@@ -193,6 +193,7 @@ _PROTOTYPES = {
     "strix_amd_plan_status": (_S, [vp, u32, C.POINTER(u32)]),
     "strix_amd_grouped_plan_status": (_S, [vp, u32, C.POINTER(u32)]),
     "strix_amd_stream_read": (_S, [vp, vp, u64, u32, vp, C.POINTER(Stream)]),
+    "strix_amd_stream_read_shaped": (_S, [vp, vp, u64, u32, u32, u32, vp, C.POINTER(Stream)]),
     "strix_amd_gemv_noalloc": (_S, [vp, C.POINTER(MatmulDesc), C.POINTER(Stream)]),
     "strix_amd_set_grouped_fold": (_S, [vp, u32]),
     "strix_amd_grouped_plan_fold": (_S, [vp, C.POINTER(u32)]),

@@ -482,12 +482,15 @@ class MoePlan:
             self.handle = None
 
 
-def stream_read(ctx, src, nbytes, workgroups, sink, stream=None):
-    """Launch the call-floor kernel: `workgroups` x 256 threads read nbytes of
-    device tensor `src` once; one word per workgroup goes to int32 tensor `sink`."""
-    abi.check(ctx.lib.strix_amd_stream_read(ctx.handle, C.c_void_p(src.data_ptr()), int(nbytes), int(workgroups),
-                                            C.c_void_p(sink.data_ptr()), C.byref(stream_desc(stream))),
-              "strix_amd_stream_read")
+def stream_read(ctx, src, nbytes, workgroups, sink, stream=None, threads=256, depth=4):
+    """Launch the streaming-read kernel: `workgroups` x `threads` threads read
+    nbytes of device tensor `src` once, `depth` 16-byte loads in flight per
+    lane; one word per workgroup (the XOR of its slice) goes to int32 tensor
+    `sink`."""
+    abi.check(ctx.lib.strix_amd_stream_read_shaped(ctx.handle, C.c_void_p(src.data_ptr()), int(nbytes),
+                                                   int(workgroups), int(threads), int(depth),
+                                                   C.c_void_p(sink.data_ptr()), C.byref(stream_desc(stream))),
+              "strix_amd_stream_read_shaped")
 
 
 def swiglu(ctx, gate, up, stream=None):

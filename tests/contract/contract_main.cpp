@@ -846,6 +846,33 @@ static void noalloc_calls(strix_context c, hipStream_t hs) {
     for (void* p : {d.x, d.y, big.x, big.y}) CHECK(hipFree(p) == hipSuccess);
 }
 
+// The streaming-read measurement kernel: every documented shape launches,
+// anything else (or a slice that is not whole 16-byte loads) is refused
+// before a launch.
+static void stream_read_calls(strix_context c, hipStream_t hs) {
+    strix_stream st = stream_of(hs);
+    const uint64_t bytes = 1 << 20;
+    void* src = device_alloc(bytes);
+    auto* sink = static_cast<uint32_t*>(device_alloc(4096 * 4));
+    for (uint32_t threads : {64u, 128u, 256u, 512u, 1024u})
+        for (uint32_t depth : {1u, 2u, 4u, 8u, 16u}) {
+            fake::launches.clear();
+            STATUS(strix_amd_stream_read_shaped(c, src, bytes, 256, threads, depth, sink, &st), STRIX_SUCCESS);
+            CHECK(fake::launches.size() == 1 && fake::launches[0].name == "stream_read");
+        }
+    fake::launches.clear();
+    STATUS(strix_amd_stream_read_shaped(c, src, bytes, 256, 96, 4, sink, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_amd_stream_read_shaped(c, src, bytes, 256, 256, 3, sink, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_amd_stream_read_shaped(c, src, bytes, 256, 2048, 4, sink, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_amd_stream_read_shaped(c, src, bytes + 16, 256, 256, 4, sink, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_amd_stream_read_shaped(c, src, bytes, 0, 256, 4, sink, &st), STRIX_ERROR_INVALID_ARGUMENT);
+    STATUS(strix_amd_stream_read_shaped(c, src, bytes, 8192, 256, 4, sink, &st), STRIX_ERROR_INSUFFICIENT_BUFFER);
+    CHECK(fake::launches.empty());
+    STATUS(strix_amd_stream_read(c, src, bytes, 512, sink, &st), STRIX_SUCCESS);
+    CHECK(fake::launches.size() == 1);
+    for (void* p : {src, static_cast<void*>(sink)}) CHECK(hipFree(p) == hipSuccess);
+}
+
 int main() {
     policy_rules();
     context_rules();
@@ -857,6 +884,7 @@ int main() {
     direct_calls(c, hs);
     moe_plan(c, hs);
     noalloc_calls(c, hs);
+    stream_read_calls(c, hs);
     // The default stream (NULL) is accepted everywhere a stream is.
     {
         const HostLinear L(128, 128, 2, false);

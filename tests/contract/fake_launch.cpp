@@ -173,9 +173,10 @@ hipError_t gemv_scratch_address(int device, void** out) {
     return hipSuccess;
 }
 
-hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t* sink,
-                              hipStream_t s) {
-    require(workgroups > 0 && bytes % (16ull * workgroups) == 0, "stream read shape", "launch_stream_read");
+hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t workgroups, uint32_t threads, uint32_t depth,
+                              uint32_t* sink, hipStream_t s) {
+    require(workgroups > 0 && bytes % (16ull * workgroups) == 0 && stream_read_shape_ok(threads, depth),
+            "stream read shape", "launch_stream_read");
     require(fake::in_live_block(src, bytes), "stream read source outside device memory", "launch_stream_read");
     require(fake::in_live_block(sink, uint64_t(workgroups) * 4), "stream read sink outside device memory",
             "launch_stream_read");

@@ -6,13 +6,14 @@ nrmse <= 3e-5; reference docs/GPU_TESTS.md:129-130), on all outputs where the
 oracle finishes in seconds and on sampled rows otherwise, plus identities that
 hold over the whole output:
 
-  * C2 GEMV 5120^2 at K4/K5/K6: R1 and R8 outputs of the prepared plan (the
-    path bench.py times) against the oracle, every output; the plan equals
-    strix_gemv bitwise; the rows of 2- and 4-row calls equal 1-row calls.
-  * C3 prefill GEMM, 5120^2 at M = 128, 512, 2048 and 4096 -> 12288 at
-    M = 128, 512: sampled rows against the oracle; a row's bits depend only on
-    its row class, so a call on the rows in reverse order returns the same
-    rows in reverse order, bit for bit.
+  * C2 GEMV 5120^2 and 4096 -> 12288 at K4/K5/K6: R1 and R8 outputs of the
+    prepared plan (the path bench.py times) against the oracle, every output;
+    the plan equals 1-row strix_gemv calls bitwise; the rows of 2- and 4-row
+    calls equal 1-row calls.
+  * C3 prefill GEMM, every cell (M = 128, 512, 2048 x 5120^2 and
+    4096 -> 12288 x K4/K5/K6): sampled rows against the oracle; a row's bits
+    depend only on its row class, so a call on the rows in reverse order
+    returns the same rows in reverse order, bit for bit.
   * C4 grouped o_a plan (16 x 4096 -> 1024, K5) at R1 and R8, both folds
     (split and owner): every output of four sampled groups against the
     oracle, all groups finite; for every row count 1-8 the owner-fold plan,
@@ -89,25 +90,54 @@ def test_c2_gemv_5120(ctx, K):
     w.destroy()
 
 
-@pytest.mark.parametrize("I,N,M,K", [(5120, 5120, 128, 4), (5120, 5120, 512, 5), (5120, 5120, 2048, 6),
-                                     (4096, 12288, 128, 6), (4096, 12288, 512, 4)])
-def test_c3_gemm(ctx, I, N, M, K):
-    print(f"C3 GEMM M={M} {I}x{N} K={K}", flush=True)
-    layer = synth.layer(I, N, K, 4800 + M + K, bias=False)
+@pytest.mark.parametrize("K", [4, 5, 6])
+def test_c2_gemv_4096_to_12288(ctx, K):
+    I, N = 4096, 12288
+    print(f"C2 GEMV {I}x{N} K={K} R1/R8", flush=True)
+    layer = synth.layer(I, N, K, 4750 + K, bias=True)
     w = runtime.Weights(ctx, *layer, "mul1")
-    x = synth.activations(M, I, 4810 + M + K)
-    y = torch.full((M, N), float("nan"), device=DEV)
-    runtime.gemm(w, _dev(x), y)
-    yr = torch.full((M, N), float("nan"), device=DEV)
-    runtime.gemm(w, _dev(x[::-1]), yr)
-    torch.cuda.synchronize()
-    got = y.cpu().numpy()
-    np.testing.assert_array_equal(yr.cpu().numpy()[::-1].view(np.uint32), got.view(np.uint32),
-                                  err_msg="row bits depend on the other rows")
-    sel = np.unique(np.r_[0:8, M // 2 - 4:M // 2 + 4, M - 8:M])
     q = codec.dequantize_rotated(layer[0], K, "mul1")
-    synth.gate(got[sel], _oracle(x[sel], layer, K, q))
-    assert np.isfinite(got).all()
+    x8 = synth.activations(8, I, 4760 + K)
+    xd = _dev(x8)
+    for R in (1, 8):
+        x = xd[:R].contiguous()
+        y = torch.full((R, N), float("nan"), device=DEV)
+        plan = runtime.LinearPlan(w, x, y)
+        plan.submit()
+        torch.cuda.synchronize()
+        plan.destroy()
+        for r in range(R):
+            y1 = torch.full((N,), float("nan"), device=DEV)
+            runtime.gemv(w, xd[r].contiguous(), y1)
+            np.testing.assert_array_equal(_bits(y1), _bits(y[r]), err_msg=f"plan R{R} row {r} vs 1-row strix_gemv")
+        synth.gate(y.cpu().numpy(), _oracle(x8[:R], layer, K, q))
+    w.destroy()
+
+
+@pytest.mark.parametrize("I,N,K", [(4096, 12288, 4), (4096, 12288, 5), (4096, 12288, 6),
+                                   (5120, 5120, 4), (5120, 5120, 5), (5120, 5120, 6)])
+def test_c3_gemm(ctx, I, N, K):
+    # Every C3 cell: M = 128, 512, 2048 on this layer.  Sampled rows (ends,
+    # the middle, a 256-row tile boundary) against the oracle; the call on the
+    # rows in reverse order returns the same rows in reverse, bit for bit.
+    layer = synth.layer(I, N, K, 4800 + I // 1024 + K, bias=False)
+    w = runtime.Weights(ctx, *layer, "mul1")
+    q = codec.dequantize_rotated(layer[0], K, "mul1")
+    for M in (128, 512, 2048):
+        print(f"C3 GEMM M={M} {I}x{N} K={K}", flush=True)
+        x = synth.activations(M, I, 4810 + M + K + I // 1024)
+        y = torch.full((M, N), float("nan"), device=DEV)
+        runtime.gemm(w, _dev(x), y)
+        yr = torch.full((M, N), float("nan"), device=DEV)
+        runtime.gemm(w, _dev(x[::-1]), yr)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        np.testing.assert_array_equal(yr.cpu().numpy()[::-1].view(np.uint32), got.view(np.uint32),
+                                      err_msg=f"M={M}: row bits depend on the other rows")
+        sel = np.unique(np.r_[0, 1, M // 2 - 1, M // 2, min(255, M - 1), min(256, M - 1), M - 2, M - 1])
+        synth.gate(got[sel], _oracle(x[sel], layer, K, q))
+        assert np.isfinite(got).all()
+        del y, yr
     w.destroy()
 
 

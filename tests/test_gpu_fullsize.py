@@ -7,7 +7,9 @@ the whole output whatever its size:
   * GEMV: every row of an 8-row call carries the bits of a 1-row call;
   * GEMM: the last 1024 rows of a 2048-row call (split-tile handoff) carry the
     bits of a 1024-row call (one K pass per tile);
-  * MoE: a token's output does not depend on the other tokens (bitwise).
+  * MoE: a token's output does not depend on the other tokens (bitwise); the
+    hidden of two slots of every token, every token's output from the GPU's
+    own hidden, and one token's whole chain meet the oracle.
 """
 import numpy as np
 import pytest
@@ -97,20 +99,24 @@ def test_c5_moe_64_experts_top8(ctx):
     for r in range(R):
         yr, _ = run(np.array([r]))
         assert np.array_equal(yr[0].view(np.uint32), y[r].view(np.uint32)), r
-    # token 0: the hidden of its first two slots against the oracle (gate and
-    # up of two experts), and its output from the GPU's own hidden (eight down
-    # projections): the single-linear gate for the latter, twice its nrmse bar
-    # for SwiGLU of two projections
+    # the hidden of every token's first and last slot against the oracle (gate
+    # and up of up to 16 experts; twice the single-linear nrmse bar for SwiGLU
+    # of two projections), every token's output from the GPU's own hidden (all
+    # 64 down projections; the single-linear gate), and token 5's whole chain
+    # from x (max-rel-err <= 1e-3 of the output's scale)
     cache = {}
-    for s in range(2):
-        e = int(ids[0, s])
-        g = moe.projection(x[:1], bank[e]["gate"], cache, (e, "gate"))
-        u = moe.projection(x[:1], bank[e]["up"], cache, (e, "up"))
-        href = moe.swiglu(g, u)[0].astype(np.float64)
-        a = hidden[0, s].astype(np.float64)
-        nrmse = np.sqrt(np.sum((a - href) ** 2) / np.sum(href ** 2))
-        assert np.max(np.abs(a - href)) <= 5e-4 * max(1.0, np.max(np.abs(href))) and nrmse <= 6e-5, (s, nrmse)
-    synth.gate(y[:1], moe.down_combine(hidden[:1], bank, ids[:1], sc[:1], cache=cache))
+    for r in range(R):
+        for s in (0, k - 1):
+            e = int(ids[r, s])
+            g = moe.projection(x[r:r + 1], bank[e]["gate"], cache, (e, "gate"))
+            u = moe.projection(x[r:r + 1], bank[e]["up"], cache, (e, "up"))
+            href = moe.swiglu(g, u)[0].astype(np.float64)
+            a = hidden[r, s].astype(np.float64)
+            nrmse = np.sqrt(np.sum((a - href) ** 2) / np.sum(href ** 2))
+            assert np.max(np.abs(a - href)) <= 5e-4 * max(1.0, np.max(np.abs(href))) and nrmse <= 6e-5, (r, s, nrmse)
+    synth.gate(y, moe.down_combine(hidden, bank, ids, sc, cache=cache))
+    chain, _ = moe.moe_block(x[5:6], bank, ids[5:6], sc[5:6], cache=cache)
+    assert np.max(np.abs(y[5] - chain[0])) <= 1e-3 * np.max(np.abs(chain[0]))
     for t in ws:
         for w in t:
             w.destroy()

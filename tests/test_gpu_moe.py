@@ -358,3 +358,42 @@ def test_split_plan_checkpoints(ctx):
             fn()
     pp.destroy()
     _destroy(ws)
+
+
+def test_down_finish_slot_order_fixed_by_arithmetic(ctx):
+    """The device's slot combine is ascending from +0, pinned by arithmetic
+    rather than by the oracle's restatement: with svh = 1, no bias and impulse
+    cores (split 0 holds v at element 0, the other splits +0), every element of
+    slot s's output is exactly v_s * c, c = RN32(1/sqrt(128)).  Terms c*2^30,
+    c, -c*2^30, 4c at unit scores sum to exactly 4c in ascending order from +0
+    (c is absorbed by c*2^30, which then cancels) and to 0 in descending order
+    or as a pairwise tree.  Zero scores drop slots; power-of-two scores scale
+    exactly."""
+    k, I, H = 4, 128, 2048
+    print(f"moe slot order pin k={k} I={I} H={H}", flush=True)
+    bank = synth.moe_bank(k, I, H, 2, 600)
+    for e in bank:
+        tr, suh, svh, _, K = e["down"]
+        e["down"] = (tr, suh, np.ones_like(svh), None, K)
+    ws = _weights(ctx, bank)
+    c = np.float32(float.fromhex("0x1.6a09e6p-4"))
+    ids = np.arange(k, dtype=np.int32)[None, :]
+    x = synth.activations(1, I, 601)
+    for scores, expect in (([1.0, 1.0, 1.0, 1.0], 4 * c), ([1.0, 0.0, 1.0, 1.0], 4 * c),
+                           ([1.0, 1.0, 1.0, 0.5], 2 * c)):
+        sc = np.array([scores], np.float32)
+        y = torch.full((1, I), float("nan"), device=DEV)
+        plan = runtime.MoePlan(ctx, ws, _dev(x), y, device_ids=_dev(ids), device_scores=_dev(sc), split=True)
+        S = plan.partials.shape[2]
+        P = np.zeros((1, k, S, I), np.float32)
+        for s, v in enumerate((2.0 ** 30, 1.0, -(2.0 ** 30), 4.0)):
+            P[0, s, 0, 0] = v
+        plan.partials.copy_(_dev(P))
+        plan.down_finish()
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()[0]
+        plan.destroy()
+        assert np.array_equal(got, np.full(I, np.float32(expect))), (scores, got[:4])
+    for t in ws:
+        for w in t:
+            w.destroy()

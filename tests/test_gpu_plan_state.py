@@ -208,13 +208,17 @@ def test_plan_after_destroy_starts_clean(ctx, reuse):
         w.destroy()
 
 
-@pytest.mark.parametrize("nbytes,wgs", [(8 << 20, 512), (1 << 20, 64), (4096, 1)])
-def test_stream_read_xor(ctx, nbytes, wgs):
-    print(f"stream read {nbytes} B x {wgs} workgroups", flush=True)
-    g = torch.Generator(device=DEV).manual_seed(nbytes + wgs)
+@pytest.mark.parametrize("nbytes,wgs,threads,depth", [(8 << 20, 512, 256, 4), (1 << 20, 64, 256, 4), (4096, 1, 256, 4),
+                                                      (8 << 20, 2048, 64, 16), (8 << 20, 256, 1024, 1),
+                                                      (1 << 20, 128, 512, 8), (160, 10, 128, 2)])
+def test_stream_read_xor(ctx, nbytes, wgs, threads, depth):
+    # Every shape reads each 16-byte word of its slice exactly once (the
+    # ring's loads past the slice read nothing).
+    print(f"stream read {nbytes} B x {wgs} workgroups x {threads} threads, depth {depth}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(nbytes + wgs + threads + depth)
     src = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device=DEV, generator=g)
     sink = torch.zeros(wgs, dtype=torch.int32, device=DEV)
-    runtime.stream_read(ctx, src, nbytes, wgs, sink)
+    runtime.stream_read(ctx, src, nbytes, wgs, sink, threads=threads, depth=depth)
     torch.cuda.synchronize()
     words = src.cpu().numpy().view(np.uint32).reshape(wgs, -1)
     expect = np.bitwise_xor.reduce(words, axis=1)

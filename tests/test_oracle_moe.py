@@ -179,3 +179,50 @@ def test_down_finish_from_split_partials():
     rev = Q.copy()
     rev[:, :, [0, 1, 2]] = Q[:, :, [2, 1, 0]]
     assert not np.array_equal(moe.down_finish(rev, bank, ids, sc)[r], yq[r])
+
+
+def _order_pin_bank(k=4, I=128, H=128):
+    """k experts whose down output stage is exactly H32 (svh = 1.0, no bias)."""
+    bank = synth.moe_bank(k, I, H, 2, 600)
+    for e in bank:
+        tr, suh, svh, bias, K = e["down"]
+        e["down"] = (tr, suh, np.ones_like(svh), None, K)
+    return bank
+
+
+def test_slot_combine_order_fixed_by_arithmetic():
+    # The slot combine is RN32(score * d_s) added in ascending slot order from
+    # +0.  Cores that are impulses (value v at element 0 of the 128-block)
+    # make every element of d_s exactly v * c, c = RN32(1/sqrt(128)): the
+    # butterflies only add zeros, and v is a power of two.  With unit scores
+    # the terms are c*2^30, c, -c*2^30, 4c.  In ascending order c is absorbed
+    # by c*2^30 (it needs 31 significant bits), the next term cancels, and the
+    # sum is 4c exactly; descending order or a pairwise tree adds the 4c or
+    # the c to -c*2^30 first, where it is absorbed, and ends at 0.
+    c = np.float32(float.fromhex("0x1.6a09e6p-4"))
+    k, I = 4, 128
+    bank = _order_pin_bank(k, I)
+    ids = np.arange(k, dtype=np.uint32)[None, :]
+    sc = np.ones((1, k), np.float32)
+    v = [2.0 ** 30, 1.0, -(2.0 ** 30), 4.0]
+    P = np.zeros((1, k, 1, I), np.float32)
+    for s in range(k):
+        P[0, s, 0, 0] = v[s]
+    y = moe.down_finish(P, bank, ids, sc)
+    assert np.array_equal(y[0], np.full(I, np.float32(4) * c)), y[0][:4]
+    # the other orders, evaluated in FP32 by hand, land on 0: the check above
+    # tells ascending order apart from them
+    t = [np.float32(x) * c for x in v]
+    desc = np.float32(0)
+    for x in reversed(t):
+        desc = np.float32(desc + x)
+    tree = np.float32(np.float32(t[0] + t[1]) + np.float32(t[2] + t[3]))
+    assert desc == 0 and tree == 0
+    # a zero score removes its slot: without slot 1 the sum is c*2^30 - c*2^30 + 4c
+    sc0 = sc.copy()
+    sc0[0, 1] = 0
+    assert np.array_equal(moe.down_finish(P, bank, ids, sc0)[0], np.full(I, np.float32(4) * c))
+    # scores scale terms exactly (powers of two): score 0.5 on slot 3 gives 2c
+    sc3 = sc.copy()
+    sc3[0, 3] = 0.5
+    assert np.array_equal(moe.down_finish(P, bank, ids, sc3)[0], np.full(I, np.float32(2) * c))
