@@ -5,8 +5,11 @@ the reference's C ABI v1, include/strix_trellis.h).  This package is the thin
 Python host layer over it:
 
 ``abi``      ctypes mirror of the C ABI (descriptors, statuses, library loader);
-``runtime``  contexts, prepared weights, GEMV/GEMM calls, plans (torch device buffers);
-``loader``   EXL3 groups mapped from local safetensors files and their transport;
+``runtime``  contexts, prepared weights, GEMV/GEMM calls, plans (on torch tensors or
+             ``device`` arrays);
+``device``   device memory and streams from the HIP runtime (ctypes), for hosts without torch;
+``loader``   EXL3 groups mapped from local safetensors files, their transport, and
+             ``Exl3Tensor.matmul(x, production=True)`` on the GPU (NumPy in and out);
 ``tp``       two-rank tensor-parallel views of EXL3 groups (rank_partition);
 ``fixture``  the STGPU001 fixture container (reader and writer).
 """

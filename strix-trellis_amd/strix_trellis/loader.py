@@ -5,7 +5,8 @@ The interface is the reference loader's (docs/LOADER.md; names
 ``SafetensorsFile``, ``Exl3Tensor``, ``load_exl3``, ``transport_regions`` /
 ``transport_buffer`` / ``transport_blob``, ``slice_outputs`` / ``slice_inputs``),
 so loading code moves over unchanged; the product path is the HIP library, so a
-group is ``prepare``d into device weights instead of multiplied on the CPU.
+group is ``prepare``d into device weights, and ``matmul(x, production=True)``
+runs on the GPU (NumPy in and out, no torch) instead of on the CPU.
 
 How it is organised here:
 
@@ -303,6 +304,52 @@ class Exl3Tensor:
         and the mapped file may be released once this returns."""
         from . import runtime
         return runtime.Weights.from_transport(ctx, self, stream=stream, blob=blob)
+
+    def matmul(self, x, *, production=False, context=None, stream=None):
+        """y = this linear applied to x: [I] -> [N] or [rows, I] -> [rows, N]
+        (reference python/strix_trellis/container.py:112-115).
+
+        production=True runs the library: strix_gemv for 1-8 rows, strix_gemm
+        above, on device weights prepared once per context and kept with this
+        tensor (``context`` defaults to ``runtime.default_context()``).  x
+        and the result are NumPy arrays (x is converted to float32); device
+        memory and the stream (``stream``, else the context's own HIP stream)
+        come from the HIP runtime through ``strix_trellis.device``, so no
+        torch is needed.  The call returns when the result has been copied
+        back.  The arithmetic is the staged FP32
+        contract of the reference's production path (matmul_fp32): input and
+        output stages bit-exact, the core within its FP64 tolerance.
+
+        production=False, the reference's FP64 algebraic matmul, is a CPU
+        mathematical reference; this library keeps it with its tests
+        (oracle/linear.py) rather than in the package, and raises
+        NotImplementedError."""
+        if not production:
+            raise NotImplementedError("the FP64 algebraic reference matmul is not part of this library; "
+                                      "matmul(x, production=True) runs the GPU path")
+        from . import device, runtime
+        xa = np.asarray(x, dtype=np.float32)
+        if xa.ndim not in (1, 2) or xa.shape[-1] != self.input_size:
+            raise ValueError(f"x must be [{self.input_size}] or [rows, {self.input_size}]")
+        rows = 1 if xa.ndim == 1 else xa.shape[0]
+        if rows == 0:
+            return np.zeros((0, self.output_size), np.float32)
+        ctx = context if context is not None else runtime.default_context()
+        s = stream if stream is not None else runtime.host_stream(ctx)
+        cache = self.__dict__.setdefault("_prepared", {})
+        if id(ctx) not in cache:
+            cache[id(ctx)] = (ctx, self.prepare(ctx, s))
+        weights = cache[id(ctx)][1]
+        dx = device.DeviceArray.from_numpy(xa, device=ctx.device)
+        dy = device.DeviceArray.empty(xa.shape[:-1] + (self.output_size,), np.float32, ctx.device)
+        ws = device.DeviceArray.empty(runtime.workspace_bytes(weights, dx, dy), np.uint8, ctx.device)
+        try:
+            (runtime.gemv if rows <= 8 else runtime.gemm)(weights, dx, dy, workspace=ws, stream=s)
+            s.synchronize()
+            return dy.numpy()
+        finally:
+            for a in (dx, dy, ws):
+                a.free()
 
 
 # ----------------------------------------------------------------------------

@@ -1,14 +1,20 @@
 """Python host layer over the C ABI (ctypes): contexts, prepared weights, calls, plans.
 
-Device buffers are PyTorch-ROCm tensors (``torch`` supplies device memory and
-streams only); every computation runs in libstrix_trellis.so.  Errors surface
-as :class:`abi.StrixError` carrying the C status.
+Device buffers are PyTorch-ROCm tensors or :class:`device.DeviceArray`
+(memory from the HIP runtime itself, for hosts without PyTorch); streams are
+torch streams or :class:`device.Stream`.  Either only supplies device memory
+and streams: every computation runs in libstrix_trellis.so.  torch is
+imported only when a torch tensor or stream is handed in (or, for the default
+stream, when the caller has imported it).  Errors surface as
+:class:`abi.StrixError` carrying the C status.
 """
 import ctypes as C
+import sys
 
 import numpy as np
 
 from . import abi
+from . import device as _hipdev
 
 _torch = None
 
@@ -21,15 +27,28 @@ def _t():
     return _torch
 
 
+def _is_torch(obj):
+    return type(obj).__module__.split(".")[0] == "torch"
+
+
 def stream_desc(stream=None):
-    """strix_stream for a torch stream (default: torch's current stream)."""
-    torch = _t()
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return abi.header(abi.Stream, hip_stream=C.c_void_p(s.cuda_stream or None))
+    """strix_stream for a torch or HIP stream.  None: torch's current stream
+    when the caller has imported torch, else the device's default (NULL)
+    stream."""
+    if stream is None:
+        torch = sys.modules.get("torch")
+        if torch is None:
+            return abi.header(abi.Stream, hip_stream=C.c_void_p(None))
+        stream = torch.cuda.current_stream()
+    return abi.header(abi.Stream, hip_stream=C.c_void_p(stream.cuda_stream or None))
+
+
+def _is_f32(t):
+    return t.dtype == (_t().float32 if _is_torch(t) else np.float32)
 
 
 def tensor_desc(t, rank=None, width=None):
-    """F32 tensor descriptor of a contiguous torch tensor (rank 1 or 2)."""
+    """F32 tensor descriptor of a contiguous torch tensor or DeviceArray (rank 1 or 2)."""
     d = abi.header(abi.TensorDesc)
     d.dtype = abi.DTYPE_F32
     if t is None:
@@ -39,7 +58,7 @@ def tensor_desc(t, rank=None, width=None):
         d.strides[0] = width or 0
         d.strides[1] = 1
         return d
-    if t.dtype != _t().float32 or not t.is_contiguous():
+    if not _is_f32(t) or not t.is_contiguous():
         raise ValueError("tensors must be contiguous float32")
     d.data = C.c_void_p(t.data_ptr() or None)
     d.buffer_bytes = t.numel() * 4
@@ -79,6 +98,28 @@ class Context:
         if self.handle:
             abi.check(self.lib.strix_context_destroy(self.handle), "strix_context_destroy")
             self.handle = None
+
+
+_DEFAULT_CONTEXTS = {}
+
+
+def default_context(device=0):
+    """A library context on `device`, created on first use and kept for the
+    process (used by ``loader.Exl3Tensor.matmul``)."""
+    if device not in _DEFAULT_CONTEXTS:
+        _DEFAULT_CONTEXTS[device] = Context(device)
+    return _DEFAULT_CONTEXTS[device]
+
+
+_HOST_STREAMS = {}
+
+
+def host_stream(ctx):
+    """A HIP stream of the context's device for NumPy-level calls
+    (``loader.Exl3Tensor.matmul``), created on first use."""
+    if id(ctx) not in _HOST_STREAMS:
+        _HOST_STREAMS[id(ctx)] = (ctx, _hipdev.Stream())
+    return _HOST_STREAMS[id(ctx)][1]
 
 
 class Weights:
@@ -244,24 +285,29 @@ def workspace_bytes(weights, x, y, rank=None):
     return out.value
 
 
-def alloc_workspace(nbytes, device):
+def alloc_workspace(nbytes, device, like=None):
+    """A workspace of at least `nbytes` bytes: a torch tensor on `device`, or a
+    DeviceArray when `like` is one (both at least 256-byte aligned)."""
+    if like is not None and not _is_torch(like):
+        return _hipdev.DeviceArray.empty(max(int(nbytes), 256), np.uint8, like.device)
     torch = _t()
     # torch's caching allocator returns 512-byte aligned blocks.
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
+
 def _on_stream(t, stream):
     """Tell torch's caching allocator that `t` is used on `stream` (when that is
     not the current stream), so its memory is not reused before the work
-    enqueued there has finished."""
-    if stream is not None and stream != _t().cuda.current_stream(t.device):
+    enqueued there has finished.  DeviceArrays are freed by their owner."""
+    if _is_torch(t) and stream is not None and _is_torch(stream) and stream != _t().cuda.current_stream(t.device):
         t.record_stream(stream)
     return t
 
 
 def _call(fn, weights, x, y, alpha, beta, workspace, stream, rank):
     if workspace is None:
-        workspace = _on_stream(alloc_workspace(workspace_bytes(weights, x, y, rank), x.device), stream)
+        workspace = _on_stream(alloc_workspace(workspace_bytes(weights, x, y, rank), x.device, x), stream)
     d = matmul_desc(weights, x, y, alpha, beta, workspace, rank)
     abi.check(fn(weights.ctx.handle, C.byref(d), C.byref(stream_desc(stream))), fn.__name__)
     return y
@@ -288,7 +334,7 @@ class LinearPlan:
     def __init__(self, weights, x, y, alpha=1.0, beta=0.0, workspace=None, stream=None, operation="gemv"):
         self.lib = weights.lib
         if workspace is None:
-            workspace = _on_stream(alloc_workspace(workspace_bytes(weights, x, y), x.device), stream)
+            workspace = _on_stream(alloc_workspace(workspace_bytes(weights, x, y), x.device, x), stream)
         self._keep = (weights, x, y, workspace)
         d = matmul_desc(weights, x, y, alpha, beta, workspace)
         op = abi.OPERATION_GEMV if operation == "gemv" else abi.OPERATION_GEMM
