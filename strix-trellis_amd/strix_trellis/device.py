@@ -82,12 +82,35 @@ def set_device(ordinal):
     check(hip().hipSetDevice(int(ordinal)), "hipSetDevice")
 
 
-class Stream:
-    """A HIP stream created on the current device (``hipStreamCreate``)."""
+def current_device():
+    d = C.c_int(0)
+    check(hip().hipGetDevice(C.byref(d)), "hipGetDevice")
+    return d.value
 
-    def __init__(self):
+
+class _on_device:
+    """Makes `ordinal` the current device for a block, then restores the previous one."""
+
+    def __init__(self, ordinal):
+        self.ordinal = int(ordinal)
+
+    def __enter__(self):
+        self.prev = current_device()
+        if self.prev != self.ordinal:
+            set_device(self.ordinal)
+
+    def __exit__(self, *exc):
+        if self.prev != self.ordinal:
+            set_device(self.prev)
+
+
+class Stream:
+    """A HIP stream (``hipStreamCreate``) on device `device` (default: the current one)."""
+
+    def __init__(self, device=None):
         h = C.c_void_p()
-        check(hip().hipStreamCreate(C.byref(h)), "hipStreamCreate")
+        with _on_device(current_device() if device is None else device):
+            check(hip().hipStreamCreate(C.byref(h)), "hipStreamCreate")
         self.cuda_stream = h.value or 0
 
     def synchronize(self):
@@ -100,16 +123,17 @@ class Stream:
 
 
 class DeviceArray:
-    """A contiguous array in device memory (one hipMalloc, 256-byte aligned)."""
+    """A contiguous array in the memory of device `device` (one hipMalloc, 256-byte aligned)."""
 
     def __init__(self, shape, dtype, device=0):
         self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
         self.dtype = np.dtype(dtype)
-        self.device = device
+        self.device = int(device)
         self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
         p = C.c_void_p()
         if self.nbytes:
-            check(hip().hipMalloc(C.byref(p), max(self.nbytes, 256)), "hipMalloc")
+            with _on_device(self.device):
+                check(hip().hipMalloc(C.byref(p), max(self.nbytes, 256)), "hipMalloc")
         self._ptr = p.value or 0
 
     # -- the surface the runtime's descriptor helpers read ----------------------

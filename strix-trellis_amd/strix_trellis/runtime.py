@@ -118,7 +118,7 @@ def host_stream(ctx):
     """A HIP stream of the context's device for NumPy-level calls
     (``loader.Exl3Tensor.matmul``), created on first use."""
     if id(ctx) not in _HOST_STREAMS:
-        _HOST_STREAMS[id(ctx)] = (ctx, _hipdev.Stream())
+        _HOST_STREAMS[id(ctx)] = (ctx, _hipdev.Stream(ctx.device))
     return _HOST_STREAMS[id(ctx)][1]
 
 
