@@ -35,6 +35,11 @@ struct GemvShape {
     uint32_t splits = 0;   // S = (I/16) / bps
 };
 GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t bits);
+// Splits whose S - 1 other planes one finisher poll round covers at eight rows
+// (two rows per wave, 32 loads per round), and the fewest workgroups a shape
+// limited to them may have.
+constexpr uint32_t kOneRoundSplits = 17;
+constexpr uint64_t kOneRoundMinWorkgroups = 384;
 
 // Bytes of the caller workspace one call needs (GEMV partial planes and the
 // FP16 core-input matrix of the GEMM path); 256-byte aligned pieces.

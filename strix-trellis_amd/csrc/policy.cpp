@@ -28,6 +28,32 @@ GemvShape gemv_shape(uint32_t input, uint32_t output, uint32_t /*bits*/) {
         const uint32_t bps = 8 * m, splits = nb / bps;
         if (uint64_t(nc) * splits >= target) best = {bps, splits};
     }
+    // A finisher wave polls two rows' other splits per round at five to eight
+    // rows, 32 loads at most, so more than 17 splits take a second coherent
+    // round trip there, and their planes a longer fold at every row count.
+    // Such a pick gives way to the most workgroups among splits of at most 17
+    // parts, if they still fill 1.5 per CU, keep at least half the splits and
+    // load the busiest CU no more (ceil(W / 256) / W, every workgroup being
+    // resident at once and sharing its CU's VALU): 5120^2 (S = 20 -> 10, 800
+    // -> 400 workgroups, 4 -> 2 on the busiest CU) measured 1 / 4 / 9 % faster
+    // at R1 / R4 / R8 (K4) and 2 / 6 / 10 % (K5).  3072 -> 4096 (768 -> 384,
+    // 3 -> 2) would load it more, and measured 4 % slower at R1 (10 % faster
+    // at R8): it keeps S = 24.
+    if (best.splits > kOneRoundSplits) {
+        constexpr uint64_t kCus = 256;
+        const uint32_t picked = best.splits;
+        const uint64_t w0 = uint64_t(nc) * picked;
+        for (uint32_t m = 1; m <= 16; ++m) {
+            if (units % m) continue;
+            const uint32_t splits = nb / (8 * m);
+            const uint64_t w1 = uint64_t(nc) * splits;
+            if (splits <= kOneRoundSplits && 2 * splits >= picked && w1 >= kOneRoundMinWorkgroups &&
+                (w1 + kCus - 1) / kCus * w0 <= (w0 + kCus - 1) / kCus * w1) {
+                best = {8 * m, splits};
+                break;
+            }
+        }
+    }
     return best;
 }
 

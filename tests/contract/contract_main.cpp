@@ -709,23 +709,52 @@ static void moe_plan(strix_context c, hipStream_t hs) {
 // tests/test_gemv_policy.cpp:92-97).  The shapes must cover their layer, stay
 // within the kernels' limits, and follow the documented choice rules.
 static void policy_rules() {
+    // The benchmark layers: C1 4096^2 S = 16, 4096 -> 12288 S = 8, 5120^2 S = 10
+    // (the one-round alternative of S = 20), grouped o_a 4096 -> 1024 S = 16.
+    CHECK(stx::gemv_shape(4096, 4096, 4).splits == 16);
+    CHECK(stx::gemv_shape(4096, 12288, 4).splits == 8);
+    CHECK(stx::gemv_shape(5120, 5120, 4).splits == 10);
+    CHECK(stx::gemv_shape(4096, 1024, 5).splits == 16);
+    CHECK(stx::gemv_shape(3072, 4096, 4).splits == 24);   // 384 workgroups would load the busiest CU more
     const uint32_t outputs[] = {128, 256, 384, 1024, 1536, 4096, 5120, 8448, 12288};
     for (uint32_t I = 128; I <= 16384; I += 128)
         for (uint32_t N : outputs) {
             // GEMV: whole 8-block units per split, at most 128 blocks; the
-            // longest split reaching 512 workgroups, else 16 or 8 blocks.
+            // longest split reaching 512 workgroups, else 16 or 8 blocks;
+            // such a pick of more than 17 splits gives way to the most
+            // workgroups (at least 384, at least half the splits, no more on
+            // the busiest CU) among splits of at most 17 parts.
             const stx::GemvShape sh = stx::gemv_shape(I, N, 4);
             const uint32_t nb = I / 16, nc = N / 128, units = nb / 8;
             CHECK(sh.bps % 8 == 0 && sh.bps >= 8 && sh.bps <= 128);
             CHECK(uint64_t(sh.bps) * sh.splits == nb);
-            const bool reaches = uint64_t(nc) * sh.splits >= 512;
-            for (uint32_t m = 1; m <= 16; ++m) {
-                if (units % m) continue;
-                const bool r = uint64_t(nc) * (nb / (8 * m)) >= 512;
-                if (reaches) CHECK(8 * m <= sh.bps || !r);   // no longer split also reaches it
-                else CHECK(!r);                              // nothing reaches it
+            auto one_round = [&](uint32_t picked) {   // bps of the one-round alternative, or 0
+                const uint64_t w0 = uint64_t(nc) * picked;
+                for (uint32_t m = 1; m <= 16; ++m) {
+                    const uint32_t s = nb / (8 * m);
+                    const uint64_t w1 = uint64_t(nc) * s;
+                    if (units % m == 0 && s <= 17 && 2 * s >= picked && w1 >= 384 &&
+                        (w1 + 255) / 256 * w0 <= (w0 + 255) / 256 * w1)
+                        return 8 * m;
+                }
+                return 0u;
+            };
+            if (sh.splits > 17) CHECK(!one_round(sh.splits));   // kept only when no one-round shape exists
+            bool replaced = false;   // sh is the one-round alternative of some pick of more than 17 splits
+            for (uint32_t p = 18; p <= 2 * sh.splits && !replaced; ++p)
+                replaced = sh.splits <= 17 && one_round(p) == sh.bps;
+            if (replaced) {
+                CHECK(uint64_t(nc) * sh.splits >= 384);
+            } else {
+                const bool reaches = uint64_t(nc) * sh.splits >= 512;
+                for (uint32_t m = 1; m <= 16; ++m) {
+                    if (units % m) continue;
+                    const bool r = uint64_t(nc) * (nb / (8 * m)) >= 512;
+                    if (reaches) CHECK(8 * m <= sh.bps || !r);   // no longer split also reaches it
+                    else CHECK(!r);                              // nothing reaches it
+                }
+                if (!reaches) CHECK(sh.bps == 8 || sh.bps == 16);
             }
-            if (!reaches) CHECK(sh.bps == 8 || sh.bps == 16);
             stx::DeviceWeights w;
             w.input = I;
             w.output = N;
