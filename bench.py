@@ -182,8 +182,9 @@ def time_rotation(rot, steps, warmup, passes=PASSES):
         rot.graph.replay()
     ok_before = rot.check()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(full + 2)]
+    warm_passes = max(1, -(-max(warmup, MIN_WARMUP) // rot.copies))
     with torch.cuda.stream(rot.stream):
-        for _ in range(max(1, -(-max(warmup, MIN_WARMUP) // rot.copies))):
+        for _ in range(warm_passes):
             rot.graph.replay()
         ev[0].record(rot.stream)
         for i in range(full):
@@ -209,7 +210,8 @@ def time_rotation(rot, steps, warmup, passes=PASSES):
     per_pass = [pe[i].elapsed_time(pe[i + 1]) / rot.copies for i in range(passes)]
     ok_passes = rot.check()
     return {"ms": total / steps, "median_pass_ms": statistics.median(per_pass), "timed_steps": steps,
-            "passes": passes, "output_check": ok_before and ok_after and ok_passes}
+            "warmup_launches": warm_passes * rot.copies, "passes": passes,
+            "output_check": ok_before and ok_after and ok_passes}
 
 
 # Launch shapes of the streaming-read kernel (threads, loads in flight per
@@ -412,7 +414,7 @@ def bench_gemv(ctx, I, N, K, R, steps, warmup, seed, oracle=False):
            "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1),
            "median_pass_us": round(t["median_pass_ms"] * 1e3, 3), "passes": t["passes"],
            **floor_fields(ctx, t["ms"] * 1e3, rot.packed, [rot.packed]), "launches": rot.launches,
-           "rotation_copies": rot.copies, "timed_steps": t["timed_steps"],
+           "rotation_copies": rot.copies, "timed_steps": t["timed_steps"], "warmup_launches": t["warmup_launches"],
            "replay_matches_eager": t["output_check"],
            "fp16_library_us": lib["us"], "speedup_vs_fp16_library": round(lib["us"] / (t["ms"] * 1e3), 2)}
     if oracle:
@@ -819,6 +821,7 @@ def main():
         "config": {"workload": "decode GEMV R1, EXL3 K4 mul1, I=N=4096, prepared single-launch plan, "
                                f"cold rotation over {head['rotation_copies']} weight copies (>=1 GiB)",
                    "us_per_call": head["us"], "median_pass_us": head["median_pass_us"], "passes": head["passes"],
+                   "warmup_launches": head["warmup_launches"],
                    "pct_hbm_peak": head["pct_hbm_peak"], "pct_read_ceiling": head["pct_read_ceiling"],
                    "replay_matches_eager": head["replay_matches_eager"],
                    "oracle_pass": head["oracle_pass"], "oracle_maxabs": head["oracle_maxabs"],
