@@ -11,12 +11,14 @@ Python host layer over it:
 ``loader``   EXL3 groups mapped from local safetensors files, their transport, and
              ``Exl3Tensor.matmul(x, production=True)`` on the GPU (NumPy in and out);
 ``tp``       two-rank tensor-parallel views of EXL3 groups (rank_partition);
-``fixture``  the STGPU001 fixture container (reader and writer).
+``fixture``  the STGPU001 fixture container (reader and writer) and the manifest
+             fixtures of EXL3 groups (``load_fixture``).
 """
 from . import abi
 from .abi import StrixError
+from .fixture import load_fixture
 from .loader import Exl3Tensor, SafetensorsFile, load_exl3
 from .tp import rank_partition
 
-__all__ = ["abi", "StrixError", "Exl3Tensor", "SafetensorsFile", "load_exl3", "rank_partition"]
+__all__ = ["abi", "StrixError", "Exl3Tensor", "SafetensorsFile", "load_exl3", "load_fixture", "rank_partition"]
 __version__ = "0.3.0"

@@ -26,8 +26,15 @@ ref         float32 [rows, N], the layer output (with bias)
 missing sections, every length against the meta dimensions, the codebook
 marker, and that no bytes trail the last section.  ``write_stgpu`` produces
 the same layout from arrays.
+
+``load_fixture`` reads the reference's other fixture form: an EXL3 group cut
+out of a published checkpoint, described by a JSON manifest (reference
+python/strix_trellis/fixture.py:11-29, tests/fixtures/eaq_v1.json).
 """
+import hashlib
+import json
 import struct
+from pathlib import Path
 
 import numpy as np
 
@@ -122,3 +129,36 @@ def write_stgpu(path, meta, arrays):
         raise ValueError("STGPU001 file would exceed 256 MiB")
     with open(path, "wb") as f:
         f.write(out)
+
+
+# ---------------------------------------------------------------------------
+# Manifest fixtures (reference python/strix_trellis/fixture.py:11-29)
+# ---------------------------------------------------------------------------
+_MANIFEST_DTYPES = {"I16": "<i2", "I32": "<i4", "F16": "<f2"}
+_MUL1_MULTIPLIER = MARKERS[CODEBOOKS.index("mul1")]
+
+
+def load_fixture(manifest, directory=None):
+    """(trellis, suh, svh, k) of the EXL3 group a fixture manifest describes.
+
+    The manifest names each tensor ``<prefix>.<part>`` with its file, byte
+    count, SHA-256, shape and dtype (I16 / I32 / F16); the files are read from
+    `directory`, else from the manifest's ``fixture_directory``.  A file whose
+    size or digest differs raises ValueError("Fixture integrity check failed:
+    <name>"), and a ``mul1`` marker other than the mul1 multiplier raises
+    ValueError("Unsupported mul1 multiplier").  k is the trellis's last
+    dimension over 16, as the reference returns it (a float).
+    """
+    meta = json.loads(Path(manifest).read_text(encoding="utf-8"))
+    base = Path(directory if directory is not None else meta["fixture_directory"])
+    parts = {}
+    for name, entry in meta["tensors"].items():
+        data = (base / entry["file"]).read_bytes()
+        if len(data) != entry["bytes"] or hashlib.sha256(data).hexdigest() != entry["sha256"]:
+            raise ValueError(f"Fixture integrity check failed: {name}")
+        part = name.rsplit(".", 1)[1]
+        parts[part] = np.frombuffer(data, dtype=_MANIFEST_DTYPES[entry["dtype"]]).reshape(entry["shape"])
+    if int(parts["mul1"].item()) & 0xFFFFFFFF != _MUL1_MULTIPLIER:
+        raise ValueError("Unsupported mul1 multiplier")
+    trellis = parts["trellis"]
+    return trellis, parts["suh"], parts["svh"], trellis.shape[-1] / 16
