@@ -17,8 +17,9 @@ Python host layer over it:
 from . import abi
 from .abi import StrixError
 from .fixture import load_fixture
-from .loader import Exl3Tensor, SafetensorsFile, load_exl3
+from .loader import Exl3Tensor, SafetensorsFile, decode_legacy_signs, load_exl3
 from .tp import rank_partition
 
-__all__ = ["abi", "StrixError", "Exl3Tensor", "SafetensorsFile", "load_exl3", "load_fixture", "rank_partition"]
+__all__ = ["abi", "StrixError", "Exl3Tensor", "SafetensorsFile", "decode_legacy_signs", "load_exl3", "load_fixture",
+           "rank_partition"]
 __version__ = "0.3.0"

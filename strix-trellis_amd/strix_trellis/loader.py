@@ -437,3 +437,15 @@ def load_exl3(file, prefix):
     bias = _bias(group, outputs)
     _disjoint(group)
     return Exl3Tensor(trellis, suh, svh, bits, codebook, bias, str(sf.path), prefix)
+
+
+def decode_legacy_signs(packed):
+    """FP16 +-1 signs of a legacy packed su/sv vector (one-dimensional 16-bit
+    words): sign 16 j + b is -1 where bit b of word j is set, else +1
+    (reference python/strix_trellis/linear.py:183-193).  Such groups carry no
+    scale contract, so ``load_exl3`` rejects them; this only unpacks the bits."""
+    words = np.asarray(packed)
+    if words.ndim != 1 or words.dtype.kind not in "iu" or words.dtype.itemsize != 2:
+        raise ValueError("Legacy signs require a one-dimensional int16/uint16 array")
+    bits = np.unpackbits(words.astype("<u2").view(np.uint8), bitorder="little")
+    return (1 - 2 * bits.astype(np.int8)).astype(np.float16)

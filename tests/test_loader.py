@@ -239,3 +239,25 @@ def test_unquantized_tensors(tmp_path):
     np.testing.assert_array_equal(f.tensor_float32("emb"), np.array([0.5, -1.0], np.float32))
     with pytest.raises(ValueError):
         f.tensor("missing")
+
+
+def test_legacy_signs_unpack_bit_b_of_word_j():
+    # Sign 16 j + b is -1 where bit b of word j is set (reference
+    # python/strix_trellis/linear.py:183-193), checked against a scalar
+    # unpacking and on words whose bits are known.
+    from strix_trellis import decode_legacy_signs
+    rng = np.random.default_rng(5)
+    words = rng.integers(0, 1 << 16, 37).astype(np.uint16)
+    signs = decode_legacy_signs(words)
+    assert signs.dtype == np.float16 and signs.shape == (37 * 16,)
+    for j, word in enumerate(words):
+        for b in range(16):
+            assert signs[16 * j + b] == (-1.0 if (int(word) >> b) & 1 else 1.0)
+    assert np.array_equal(decode_legacy_signs(words.view(np.int16)), signs)
+    known = decode_legacy_signs(np.array([0x0001, 0x8000, 0xFFFF, 0], dtype=np.uint16))
+    assert known[0] == -1 and (known[1:16] == 1).all()
+    assert (known[16:31] == 1).all() and known[31] == -1
+    assert (known[32:48] == -1).all() and (known[48:] == 1).all()
+    for bad in (np.zeros((2, 2), np.uint16), np.zeros(4, np.uint32), np.zeros(4, np.float16)):
+        with pytest.raises(ValueError, match="one-dimensional int16/uint16"):
+            decode_legacy_signs(bad)
