@@ -12,7 +12,8 @@
 //
 // Plan-owned device memory (one allocation, freed by destroy): the bank
 // table, the uploaded routes of a host-route plan, the arrival counters (zero
-// between submissions) and the split partial planes.  The caller's workspace
+// between submissions), the split partial planes and the routes' FP16 gate/up
+// core inputs [rows*k][2][I].  The caller's workspace
 // holds hidden F32 [rows][k][H], as in the reference.  A split plan (the
 // split creators) keeps its down planes in the caller's workspace instead,
 // as P F32 [rows][k][S][I] from the first 256-byte boundary after hidden, the
@@ -250,9 +251,10 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     const uint64_t counter_bytes = align_up(counter_words * 4);
     const uint64_t partial_bytes = align_up(
         (split ? stx::moe_gate_up_partial_floats(routes, a.I, a.H) : stx::moe_partial_floats(routes, a.I, a.H)) * 4);
+    const uint64_t input_bytes = align_up(stx::moe_core_input_bytes(routes, a.I));
     auto* p = new (std::nothrow) strix_tp_moe_plan_impl;
     if (!p) return STRIX_ERROR_OUT_OF_MEMORY;
-    hipError_t e = hipMalloc(&p->device, table_bytes + route_bytes + counter_bytes + partial_bytes);
+    hipError_t e = hipMalloc(&p->device, table_bytes + route_bytes + counter_bytes + partial_bytes + input_bytes);
     if (e != hipSuccess) {
         delete p;
         return e == hipErrorOutOfMemory ? STRIX_ERROR_OUT_OF_MEMORY : status_of(e);
@@ -277,6 +279,8 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     a.p_d = split ? reinterpret_cast<float*>(static_cast<char*>(d->workspace) + v.p_offset)
                   : a.p_gu + stx::moe_gate_up_partial_floats(routes, a.I, a.H);
     a.hidden = static_cast<float*>(d->workspace);
+    cursor += partial_bytes;
+    a.a_gu = reinterpret_cast<uint16_t*>(cursor);
     const hipError_t done = hipStreamSynchronize(hs);
     if (e != hipSuccess || done != hipSuccess) {
         (void)hipFree(p->device);

@@ -18,8 +18,40 @@ static bool moe_args_ok(const MoeArgs& a) {
            a.bps_gu * a.s_gu * 16 == a.I && a.bps_d * a.s_d * 16 == a.H;
 }
 
+// Core inputs of the gate and up projections, once per route j:
+// a_gu[j][p] = RN16(H32(RN16(RN32(x[j / k] * suh_p)))) with the suh of the
+// route's expert, p = gate (0) or up (1); the values and bits of the gate/up
+// core's own input stage (input_values).  Wave w of workgroup (bx, j) takes
+// 128-block 4 bx + w.  A route whose id is outside the bank writes nothing:
+// its token is invalid, and the gate/up launch reads only valid tokens' routes.
+__global__ __launch_bounds__(GEMV_THREADS) void moe_input_kernel(MoeArgs a) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint32_t j = blockIdx.y, b = blockIdx.x * GEMV_WAVES + uint32_t(w);
+    if (b >= a.I / 128) return;
+    const float* xr = a.x + uint64_t(j / a.topk) * a.x_stride + 128 * b;
+    const float x0 = ld_global(xr + lane), x1 = ld_global(xr + lane + 64);   // issued ahead of the id's round trip
+    const uint32_t e = moe_first(ld_global(a.ids + j));
+    if (e >= a.bank_count) return;
+    const MoeExpert& ex = a.bank[e];
+    const uint32_t n0 = 128 * b + lane;
+    const InputLoad lg{x0, x1, ld_global(ex.gate.suh + n0), ld_global(ex.gate.suh + n0 + 64)};
+    const InputLoad lu{x0, x1, ld_global(ex.up.suh + n0), ld_global(ex.up.suh + n0 + 64)};
+    _Float16 g0, g1, u0, u1;
+    input_values(lg, g0, g1);
+    input_values(lu, u0, u1);
+    uint16_t* out = a.a_gu + uint64_t(j) * 2 * a.I;
+    out[n0] = __builtin_bit_cast(uint16_t, g0);
+    out[n0 + 64] = __builtin_bit_cast(uint16_t, g1);
+    out[a.I + n0] = __builtin_bit_cast(uint16_t, u0);
+    out[a.I + n0 + 64] = __builtin_bit_cast(uint16_t, u1);
+}
+
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t stream) {
-    if (!moe_args_ok(a)) return hipErrorInvalidValue;
+    if (!moe_args_ok(a) || !a.a_gu) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_input_kernel, dim3((a.I / 128 + GEMV_WAVES - 1) / GEMV_WAVES, a.rows * a.topk),
+                       dim3(GEMV_THREADS), 0, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     return gate_up_table[a.gate_bits - 2](a, stream);
 }
 

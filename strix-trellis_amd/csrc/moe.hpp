@@ -37,6 +37,7 @@ struct MoeArgs {
     float* hidden;            // [rows][k][H] F32
     float* p_gu;              // [rows*k][s_gu][2][H] partial planes of gate (0) and up (1)
     float* p_d;               // [rows*k][s_d][I] partial planes of down
+    uint16_t* a_gu;           // [rows*k][2][I] FP16 core inputs of gate (0) and up (1), per route
     uint32_t* c_gu;           // [rows*k][H/128] arrival counters, zero between launches
     uint32_t* c_d;            // [rows][I/128]
     uint64_t x_stride, y_stride;
@@ -69,8 +70,12 @@ MoeSplit moe_split(uint32_t input, uint32_t max_bps);
 uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
 uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H);
 
+// Gate/up: the routes' core inputs (one launch), then the expert cores and
+// SwiGLU (a second launch that reads them).
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t stream);
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t stream);
+// Bytes of a_gu for `routes` routes of input width I.
+constexpr uint64_t moe_core_input_bytes(uint32_t routes, uint32_t I) { return uint64_t(routes) * 2 * I * 2; }
 // Staged down: the core alone in `mode` (kMoeDownCore or kMoeDownRouteCore),
 // and the finish alone, which folds the planes p_d as they are in memory
 // (ascending split from +0, output stage, ordered score-weighted slot sum,

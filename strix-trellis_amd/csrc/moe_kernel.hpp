@@ -347,27 +347,28 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
     auto offg = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbg + og : kOut; };
     auto offu = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rbu + ou : kOut; };
 
-    // Input stages (gate and up have their own suh): one 128-block per wave and
-    // unit, the loads of MOE_UNITS units per wave in flight together.  The
-    // first batch is loaded before the weight prefetch: vector loads complete
-    // in issue order, so loads issued after the chunks would wait for the
-    // chunks' HBM round trip.
-    const int hblocks = int(bps) / 8, per_proj = nrows * hblocks, units = 2 * per_proj;
-    auto unit_load = [&](int u) -> InputLoad {
-        const int p = u / per_proj, v = u - p * per_proj;
-        const int i = v / hblocks, hb = v - i * hblocks;
-        const uint32_t r = moe_nth_route(active, i) / a.topk;
-        const uint32_t ch = a0 * 16 + hb * 128;
-        const uint16_t* suh = p ? ex.up.suh : ex.gate.suh;
-        return input_load(a.x + r * a.x_stride + ch, suh + ch, true);
-    };
-    auto unit_out = [&](int u) -> _Float16* {
-        const int p = u / per_proj, v = u - p * per_proj;
-        const int i = v / hblocks, hb = v - i * hblocks;
-        return act + (p * MOE_MAX_RT + i) * act_row + hb * 128;
-    };
-    InputLoad pre[MOE_UNITS];
-    moe_batch_load(w, units, pre, unit_load);
+    // Core inputs of the split's channels, computed once per route by
+    // moe_input_kernel (every column group of an expert used to recompute
+    // them): one 256-byte unit per (projection, row, 128-block), 4 bytes per
+    // lane, straight into LDS by DMA, no registers in flight.  Issued before
+    // the weight prefetch: vector loads complete in issue order, so loads
+    // issued after the chunks would wait for the chunks' HBM round trip.
+    // Wave w takes 128-blocks w, w + 4, ... of every row and projection
+    // (scalar loops, no divisions).
+    const int hblocks = int(bps) / 8;
+    const auto ars = make_rsrc(a.a_gu, uint32_t(moe_core_input_bytes(a.rows * a.topk, a.I)));
+    uint64_t left = active;
+    for (int i = 0; i < nrows; ++i) {   // wave-uniform
+        const uint32_t j = uint32_t(__builtin_ctzll(left));
+        left &= left - 1;
+        for (int p = 0; p < 2; ++p)
+            for (int hb = w; hb < hblocks; hb += GEMV_WAVES) {
+                const uint32_t src = ((j * 2 + uint32_t(p)) * a.I + a0 * 16 + uint32_t(hb) * 128) * 2;
+                _Float16* dst = act + (p * MOE_MAX_RT + i) * act_row + hb * 128;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 4,
+                                                         uint32_t(lane) * 4u, src, 0, 0);
+            }
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     Chunk<KG> cg[MOE_RING_GU];
@@ -377,8 +378,12 @@ __device__ __forceinline__ void moe_gate_up_core(const MoeArgs& a, const MoeExpe
         load_chunk(cg[u], rg, offg(u));
         load_chunk(cu[u], ru, offu(u));
     }
-
-    moe_input_stage(w, units, pre, unit_load, unit_out);
+    __builtin_amdgcn_sched_barrier(0);
+    // The compiler does not see the DMAs' LDS side: wait for them by count
+    // (the 2 x MOE_RING_GU chunk loads, one instruction each at K <= 3, were
+    // issued after them), then the barrier makes every wave's units visible.
+    static_assert(KG <= 3 && KU <= 3, "one load instruction per chunk");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * MOE_RING_GU) : "memory");
     // Rows past nrows stay unused: rows nrows..RT-1 hold stale LDS, their
     // columns of the products are independent of the others, and the fold
     // below reads only rows < nrows.

@@ -197,6 +197,8 @@ static void check_moe(const MoeArgs& a, bool gate_up, const char* who) {
         for (uint64_t i = 0; i < words; ++i) require(a.c_gu[i] == 0, "gate/up counters not zero on entry", who);
         require(fake::in_live_block(a.p_gu, routes * a.s_gu * 2 * a.H * 4), "gate/up planes outside device memory",
                 who);
+        require(fake::in_live_block(a.a_gu, moe_core_input_bytes(uint32_t(routes), a.I)),
+                "gate/up core inputs outside device memory", who);
     } else {
         require(fake::in_live_block(a.y, ((a.rows - 1) * a.y_stride + a.I) * 4), "output outside device memory", who);
         const uint64_t words = uint64_t(a.rows) * (a.I / 128);
