@@ -521,7 +521,7 @@ def bench_moe(ctx, steps, warmup, seed):
             "median_pass_us": round(t["median_pass_ms"] * 1e3, 2), "passes": t["passes"],
             "packed_GBps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1),
             **floor_fields(ctx, t["ms"] * 1e3, rot.packed, [gu, dn]),
-            "call_floor_launches": "gate/up bytes, then down bytes, each in its fastest shape", "launches": 2,
+            "call_floor_launches": "gate/up bytes, then down bytes, each in its fastest shape", "launches": 3,
             "rotation_copies": rot.copies, "timed_steps": t["timed_steps"],
             "replay_matches_eager": t["output_check"]}
 
