@@ -31,9 +31,11 @@ ARCH = "gfx950"
 
 COMMON = ["-O3", "-std=c++20", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra",
           f"-I{ROOT / 'include'}", f"-I{CSRC}"]
-# Packed FP32 VALU ops are kept out of all device code.
+# Packed FP32 VALU ops are kept out of all device code.  Leading scalar
+# kernel arguments are preloaded into SGPRs by the dispatcher (the GEMV passes
+# its first-needed fields that way).
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-fno-gpu-flush-denormals-to-zero"]
+          "-fno-gpu-flush-denormals-to-zero", "-mllvm", "-amdgpu-kernarg-preload-count=16"]
 HOST = ["-x", "c++", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}"]
 
 

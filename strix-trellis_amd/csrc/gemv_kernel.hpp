@@ -468,17 +468,62 @@ __device__ __forceinline__ void mfma_partials(const MfmaAcc<RT>& acc, float* red
 template <int K, int RT>
 constexpr int gemv_waves_per_eu() { return (RT == 8 && K >= 6) || (RT == 6 && K == 8) ? 4 : 5; }
 
+// The fields every workgroup needs before its first memory access come as
+// scalar arguments ahead of GemvArgs (16-bit pairs where the values fit), so
+// that the dispatcher preloads them into SGPRs (kernel-argument preloading,
+// built with -amdgpu-kernarg-preload-count); a by-value struct is never
+// preloaded, and each workgroup would otherwise wait for a scalar load of its
+// arguments before issuing any load of its own.  The rest of GemvArgs is
+// needed later.  Same bits; with nothing else read from memory ahead of the
+// first loads (below) measured 3.8 % faster on C1 (7.20 -> 6.93 us) and 1-4 %
+// on 4096 -> 12288 and 5120^2 at R1-R8.
 template <int K, int CB, int RT>
 __global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu<K, RT>())))
-void gemv_kernel(GemvArgs a) {
+void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, uint32_t* epochs,
+                 const GroupWeights* table, uint32_t ncg_groups, uint32_t bps_splits, uint32_t rows_mode, uint32_t n,
+                 uint32_t x_row_stride, GemvArgs args) {
+    GemvArgs a = args;
+    a.w.trellis = trellis;
+    a.w.suh = suh;
+    a.x = x0;
+    a.state.epochs = epochs;
+    a.table = table;
+    a.ncg = ncg_groups & 0xFFFFu;
+    a.groups = ncg_groups >> 16;
+    a.bps = bps_splits & 0xFFFFu;
+    a.splits = bps_splits >> 16;
+    a.rows = rows_mode & 0xFFu;
+    a.mode = (rows_mode >> 8) & 0xFFu;
+    // Workgroups below this index wait for their input before most of their
+    // weight ring (the two-round ordering below); computed on the host, so
+    // no workgroup reads the grid size from memory first.
+    const uint32_t first_round_end = rows_mode >> 16;
+    a.N = n;
+    a.x_row_stride = x_row_stride;
     extern __shared__ __align__(16) unsigned char smem[];
     const GemvSlot place = gemv_slot(a);
     const int c = int(place.c), s = int(place.s), z = int(place.z);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int jt = lane >> 3, g = lane & 7;
-    const GroupWeights gw = group_weights(a, z);
-    const float* x = a.x + z * a.x_group_stride;
-    float* y = a.y + z * a.y_group_stride;
+    // Up to its first loads a single-group launch uses preloaded arguments
+    // only (trellis, suh, x); a grouped launch reads its group's weights from
+    // the table.  svh, bias and y, needed at the finish only, are taken there
+    // (gw_finish, y_of), so that no wait for the rest of GemvArgs sits ahead
+    // of the first loads.
+    GroupWeights gw{trellis, suh, nullptr, nullptr};
+    const float* x = x0;
+    if (table) {
+        gw.trellis = table[z].trellis;
+        gw.suh = table[z].suh;
+        x = x0 + uint64_t(z) * a.x_group_stride;
+    }
+    auto gw_finish = [&]() {
+        GroupWeights f = gw;
+        f.svh = table ? table[z].svh : args.w.svh;
+        f.bias = table ? table[z].bias : args.w.bias;
+        return f;
+    };
+    auto y_of = [&]() { return a.y + uint64_t(z) * a.y_group_stride; };
 
     constexpr uint32_t tile_bytes = 32u * K;
     const uint32_t row_bytes = (a.N >> 4) * tile_bytes;
@@ -556,7 +601,7 @@ void gemv_kernel(GemvArgs a) {
     Chunk<K> ring[4];
     load_chunk(ring[0], rsrc, block_off(0));
     __builtin_amdgcn_sched_barrier(0);
-    if (gridDim.x <= 2 * kGemvCus && blockIdx.x + kGemvCus < gridDim.x) {
+    if (blockIdx.x < first_round_end) {
         // every load but block 0's (one instruction for K <= 4, two above)
         if constexpr (K <= 4) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
@@ -626,13 +671,14 @@ void gemv_kernel(GemvArgs a) {
     if (a.splits == 1) {
         // Loading the output-stage operands in the prologue instead keeps them
         // live across the main loop and made the 1-row kernel spill (slower).
-        const ColumnOperands op = column_operands(gw, c, a.N);
+        const GroupWeights gf = gw_finish();
+        const ColumnOperands op = column_operands(gf, c, a.N);
         lds_barrier();
-        finish_columns(a, gw, op, y, c, 1, [&](int, int r) -> const float* { return red + r * 128; });
+        finish_columns(a, gf, op, y_of(), c, 1, [&](int, int r) -> const float* { return red + r * 128; });
         return;
     }
     lds_barrier();
-    finish_polled<RT>(a, gw, y, c, red, flag, cur, epoch, place.cz);
+    finish_polled<RT>(a, gw_finish(), y_of(), c, red, flag, cur, epoch, place.cz);
 }
 
 // ---------------------------------------------------------------------------
@@ -814,7 +860,8 @@ hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t 
 #define STX_INSTANTIATE_GEMV(K)                                                                           \
     template <>                                                                                           \
     hipError_t gemv_dispatch<K>(const GemvLaunch& l) {                                                    \
-        using Fn = void (*)(GemvArgs);                                                                    \
+        using Fn = void (*)(const uint32_t*, const uint16_t*, const float*, uint32_t*, const GroupWeights*,  \
+                            uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, GemvArgs);                   \
         static const Fn table[3][6] = {                                                                   \
             {gemv_kernel<K, 0, 1>, gemv_kernel<K, 0, 2>, gemv_kernel<K, 0, 3>, gemv_kernel<K, 0, 4>,      \
              gemv_kernel<K, 0, 6>, gemv_kernel<K, 0, 8>},                                                 \
@@ -824,7 +871,17 @@ hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t 
              gemv_kernel<K, 2, 6>, gemv_kernel<K, 2, 8>}};                                                \
         const int rt = int(l.rows_template);                                                              \
         const int ri = rt <= 4 ? rt - 1 : rt == 6 ? 4 : 5;                                                \
-        hipLaunchKernelGGL(table[l.codebook][ri], l.grid, dim3(GEMV_THREADS), l.lds, l.stream, l.args);   \
+        const GemvArgs& a = l.args;                                                                       \
+        if (a.ncg > 0xFFFFu || a.groups > 0xFFFFu || a.bps > 0xFFFFu || a.splits > 0xFFFFu ||             \
+            a.rows > 0xFFu || a.mode > 0xFFu || a.x_row_stride > 0xFFFFFFFFull)                           \
+            return hipErrorInvalidValue;                                                                  \
+        /* two dispatch rounds (257..512 workgroups): the first round ends at grid - 256 */               \
+        const uint32_t gx = l.grid.x;                                                                     \
+        const uint32_t fre = gx > kGemvCus && gx <= 2 * kGemvCus ? gx - kGemvCus : 0u;                    \
+        hipLaunchKernelGGL(table[l.codebook][ri], l.grid, dim3(GEMV_THREADS), l.lds, l.stream, a.w.trellis, \
+                           a.w.suh, a.x, a.state.epochs, a.table, a.ncg | (a.groups << 16),                \
+                           a.bps | (a.splits << 16), a.rows | (a.mode << 8) | (fre << 16), a.N,           \
+                           uint32_t(a.x_row_stride), a);                                                  \
         return hipGetLastError();                                                                         \
     }                                                                                                     \
     template <>                                                                                           \
