@@ -24,7 +24,17 @@ static bool moe_args_ok(const MoeArgs& a) {
 // core's own input stage (input_values).  Wave w of workgroup (bx, j) takes
 // 128-block 4 bx + w.  A route whose id is outside the bank writes nothing:
 // its token is invalid, and the gate/up launch reads only valid tokens' routes.
-__global__ __launch_bounds__(GEMV_THREADS) void moe_input_kernel(MoeArgs a) {
+__global__ __launch_bounds__(GEMV_THREADS) void moe_input_kernel(const float* x, const uint32_t* ids,
+                                                                 const MoeExpert* bank, uint32_t topk,
+                                                                 uint32_t bank_count, uint32_t x_stride, MoeArgs args) {
+    // Everything its first loads need is preloaded (scalar arguments).
+    MoeArgs a = args;
+    a.x = x;
+    a.ids = ids;
+    a.bank = bank;
+    a.topk = topk;
+    a.bank_count = bank_count;
+    a.x_stride = x_stride;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const uint32_t j = blockIdx.y, b = blockIdx.x * GEMV_WAVES + uint32_t(w);
     if (b >= a.I / 128) return;
@@ -48,8 +58,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_input_kernel(MoeArgs a) {
 
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t stream) {
     if (!moe_args_ok(a) || !a.a_gu) return hipErrorInvalidValue;
+    if (a.x_stride > 0xFFFFFFFFull) return hipErrorInvalidValue;
     hipLaunchKernelGGL(moe_input_kernel, dim3((a.I / 128 + GEMV_WAVES - 1) / GEMV_WAVES, a.rows * a.topk),
-                       dim3(GEMV_THREADS), 0, stream, a);
+                       dim3(GEMV_THREADS), 0, stream, a.x, a.ids, a.bank, a.topk, a.bank_count,
+                       uint32_t(a.x_stride), a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return gate_up_table[a.gate_bits - 2](a, stream);

@@ -425,7 +425,18 @@ constexpr int moe_waves_per_eu(int bits_sum, int projections) { return bits_sum 
 // largest split), so that five workgroups fit a CU.
 template <int KG, int KU>
 __global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(moe_waves_per_eu(KG + KU, 2))))
-void moe_gate_up_kernel(MoeArgs a) {
+void moe_gate_up_kernel(const uint32_t* ids, const float* scores, const MoeExpert* bank, uint32_t rows_topk,
+                        uint32_t bank_count, MoeArgs args) {
+    // The route resolution's inputs and the bank come as scalar arguments, so
+    // the dispatcher preloads them into SGPRs and the first loads (the routes)
+    // wait for no argument load (the rest of MoeArgs is needed after them).
+    MoeArgs a = args;
+    a.ids = ids;
+    a.scores = scores;
+    a.bank = bank;
+    a.rows = rows_topk & 0xFFFFu;
+    a.topk = rows_topk >> 16;
+    a.bank_count = bank_count;
     __shared__ __align__(16) unsigned char lds[moe_max(MOE_GU_ACT_BYTES, MOE_GU_RED_BYTES)];
     _Float16* act = reinterpret_cast<_Float16*>(lds);
     float* red = reinterpret_cast<float*>(lds);
@@ -630,7 +641,16 @@ __device__ __forceinline__ void moe_finish_token(const MoeArgs& a, uint32_t r, u
 
 template <int K>
 __global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(moe_waves_per_eu(K, 1))))
-void moe_down_kernel(MoeArgs a) {
+void moe_down_kernel(const uint32_t* ids, const float* scores, const MoeExpert* bank, uint32_t rows_topk,
+                     uint32_t bank_count, MoeArgs args) {
+    // Preloaded resolution inputs, as in the gate/up kernel.
+    MoeArgs a = args;
+    a.ids = ids;
+    a.scores = scores;
+    a.bank = bank;
+    a.rows = rows_topk & 0xFFFFu;
+    a.topk = rows_topk >> 16;
+    a.bank_count = bank_count;
     __shared__ __align__(16) unsigned char lds[moe_max(MOE_D_ACT_BYTES, MOE_D_RED_BYTES)];
     _Float16* act = reinterpret_cast<_Float16*>(lds);
     float* red = reinterpret_cast<float*>(lds);
@@ -704,16 +724,19 @@ void moe_down_kernel(MoeArgs a) {
     template <>                                                                                                   \
     hipError_t moe_gate_up_dispatch<KG>(const MoeArgs& a, hipStream_t s) {                                        \
         const dim3 grid(a.H / 128, a.s_gu, a.rows * a.topk);                                                      \
+        const uint32_t rk = a.rows | (a.topk << 16);                                                              \
         if (a.up_bits == 2)                                                                                       \
-            hipLaunchKernelGGL((moe_gate_up_kernel<KG, 2>), grid, dim3(GEMV_THREADS), 0, s, a);                     \
+            hipLaunchKernelGGL((moe_gate_up_kernel<KG, 2>), grid, dim3(GEMV_THREADS), 0, s, a.ids, a.scores,       \
+                               a.bank, rk, a.bank_count, a);                                                      \
         else                                                                                                      \
-            hipLaunchKernelGGL((moe_gate_up_kernel<KG, 3>), grid, dim3(GEMV_THREADS), 0, s, a);                     \
+            hipLaunchKernelGGL((moe_gate_up_kernel<KG, 3>), grid, dim3(GEMV_THREADS), 0, s, a.ids, a.scores,       \
+                               a.bank, rk, a.bank_count, a);                                                      \
         return hipGetLastError();                                                                                 \
     }                                                                                                             \
     template <>                                                                                                   \
     hipError_t moe_down_dispatch<KG>(const MoeArgs& a, hipStream_t s) {                                           \
         hipLaunchKernelGGL(moe_down_kernel<KG>, dim3(a.I / 128, a.s_d, a.rows * a.topk), dim3(GEMV_THREADS), 0, s, \
-                           a);                                                                                    \
+                           a.ids, a.scores, a.bank, a.rows | (a.topk << 16), a.bank_count, a);                    \
         return hipGetLastError();                                                                                 \
     }
 
