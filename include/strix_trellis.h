@@ -423,7 +423,9 @@ strix_status strix_tp_moe_plan_create_device(strix_context context,
     strix_tp_moe_plan *out);
 /* Split plans: the workspace holds hidden F32 [rows][k][H] and, from the next
  * 256-byte boundary, P F32 [rows][k][S][I], the down core's per-split partial
- * sums (S = its split count for input width H).  Every down of a split plan
+ * sums.  S = 4 with split s over input blocks [s T / 4, (s + 1) T / 4) of the
+ * T = H / 16 blocks, as in the reference, for every H up to 5120 (and larger H
+ * whose parts fit the kernel; else the down core's own split count).  Every down of a split plan
  * writes P for each computed route (valid token, non-zero score).  The staged
  * calls (split plans only): down_core writes P alone, down_finish folds P as
  * the caller leaves it into the output, down_reference_core recomputes P one

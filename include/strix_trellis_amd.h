@@ -59,8 +59,8 @@ strix_status strix_amd_swiglu(strix_context context, const float *gate, const fl
  * strix_tp_moe_workspace_bytes (split = 0) and strix_tp_moe_split_workspace_bytes
  * (split != 0) for strix_tp_moe_device_desc, with the same validation as
  * strix_tp_moe_plan_create_device.  Plain plans need hidden F32 [rows][k][H];
- * split plans add P F32 [rows][k][S][I] from the next 256-byte boundary, S the
- * down core's split count for input width H. */
+ * split plans add P F32 [rows][k][S][I] from the next 256-byte boundary, with
+ * the split count of strix_tp_moe_split_workspace_bytes (S = 4 up to H = 5120). */
 strix_status strix_amd_tp_moe_device_workspace_bytes(strix_context context,
     const strix_tp_moe_device_desc *desc, uint32_t split, uint64_t *out_bytes);
 

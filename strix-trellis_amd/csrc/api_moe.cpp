@@ -17,7 +17,8 @@
 // holds hidden F32 [rows][k][H], as in the reference.  A split plan (the
 // split creators) keeps its down planes in the caller's workspace instead,
 // as P F32 [rows][k][S][I] from the first 256-byte boundary after hidden, the
-// staged checkpoint the reference's split3 plans expose there: every down
+// staged checkpoint the reference's split plans expose there, with the
+// reference's four equal parts of the down input (moe_split_staged): every down
 // (fused or staged core) writes P of each computed route, and the staged
 // finish folds P as the caller leaves it.
 #include "api_internal.hpp"
@@ -145,8 +146,9 @@ strix_status common_check(strix_context c, const D* d, uint64_t routes_per_row, 
     a.x = static_cast<const float*>(d->input.data);
     a.y = static_cast<float*>(d->output.data);
     v.hidden_bytes = rows * routes_per_row * H * sizeof(float);
+    // A split plan's down runs the staged partition, whose planes are P.
     v.p_offset = align_up(v.hidden_bytes);
-    v.p_bytes = stx::moe_down_partial_floats(uint32_t(rows * routes_per_row), I, H) * sizeof(float);
+    v.p_bytes = rows * routes_per_row * stx::moe_split_staged(H).splits * uint64_t(I) * sizeof(float);
     return STRIX_SUCCESS;
 }
 
@@ -244,6 +246,11 @@ strix_status create_plan(strix_context c, const D* d, hipStream_t hs, MoeValidat
     if ((s = device_resident(c, Span(d->workspace, d->workspace_bytes), kWorkspaceAlign)) != STRIX_SUCCESS) return s;
 
     stx::MoeArgs& a = v.args;
+    if (split) {
+        const stx::MoeSplit sd = stx::moe_split_staged(a.H);
+        a.s_d = sd.splits;
+        a.bps_d = sd.bps;
+    }
     const uint32_t routes = a.rows * a.topk;
     const uint64_t table_bytes = align_up(v.bank.size() * sizeof(stx::MoeExpert));
     const uint64_t route_bytes = v.ids.empty() ? 0 : 2 * align_up(uint64_t(routes) * 4);

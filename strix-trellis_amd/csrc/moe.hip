@@ -10,12 +10,15 @@ static const MoeDispatch down_table[2] = {moe_down_dispatch<2>, moe_down_dispatc
 
 static bool moe_args_ok(const MoeArgs& a) {
     const uint32_t routes = a.rows * a.topk;
+    // Down splits may start and end inside a 128-channel group; the groups a
+    // split touches must fit the down kernel's activation buffer.
+    bool down_fits = a.bps_d >= 1 && a.s_d >= 1 && a.s_d <= a.H / 16;
+    for (uint32_t s = 0; down_fits && s < a.s_d; ++s) down_fits = moe_down_groups(a.bps_d, s) <= uint32_t(MOE_D_MAX_BPS) / 8;
     return a.rows >= 1 && a.rows <= 8 && a.topk >= 1 && a.topk <= MOE_MAX_TOPK && routes <= MOE_MAX_ROUTES &&
            a.bank_count >= 1 && a.bank_count <= MOE_MAX_BANK &&
            a.I % 128 == 0 && a.H % 128 == 0 && a.gate_bits >= 2 && a.gate_bits <= 3 && a.up_bits >= 2 &&
            a.up_bits <= 3 && a.down_bits >= 2 && a.down_bits <= 3 && a.bps_gu <= uint32_t(MOE_GU_MAX_BPS) &&
-           a.bps_d <= uint32_t(MOE_D_MAX_BPS) && a.bps_gu % 8 == 0 && a.bps_d % 8 == 0 &&
-           a.bps_gu * a.s_gu * 16 == a.I && a.bps_d * a.s_d * 16 == a.H;
+           a.bps_gu % 8 == 0 && down_fits && a.bps_gu * a.s_gu * 16 == a.I && a.bps_d * a.s_d * 16 == a.H;
 }
 
 // Core inputs of the gate and up projections, once per route j:

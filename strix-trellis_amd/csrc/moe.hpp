@@ -67,6 +67,15 @@ struct MoeSplit {
 constexpr int MOE_GU_MAX_BPS = 64;   // gate/up: input I
 constexpr int MOE_D_MAX_BPS = 96;    // down: input H
 MoeSplit moe_split(uint32_t input, uint32_t max_bps);
+// 128-channel groups that down split s touches: its blocks are
+// [s bps, (s + 1) bps), which need not start or end on a group boundary.
+constexpr uint32_t moe_down_groups(uint32_t bps, uint32_t s) { return (s * bps + bps + 7) / 8 - (s * bps) / 8; }
+// Down split of a split plan, whose planes P [rows][k][S][I] are the staged
+// checkpoint: the reference's four equal parts of the T = H / 16 input blocks,
+// split s over blocks [s T / 4, (s + 1) T / 4) (reference
+// src/tp_fused_layout.hpp:19-24, P indexed as src/tp_moe_split_layout.hpp:119-122),
+// when every part's groups fit the down kernel's LDS; otherwise moe_split.
+MoeSplit moe_split_staged(uint32_t H);
 uint64_t moe_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
 uint64_t moe_counter_words(uint32_t rows, uint32_t routes, uint32_t I, uint32_t H);
 
@@ -83,7 +92,7 @@ constexpr uint64_t moe_core_input_bytes(uint32_t routes, uint32_t I) { return ui
 hipError_t launch_moe_down_core(const MoeArgs& a, MoeDownMode mode, hipStream_t stream);
 hipError_t launch_moe_down_finish(const MoeArgs& a, hipStream_t stream);
 uint64_t moe_gate_up_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
-uint64_t moe_down_partial_floats(uint32_t routes, uint32_t I, uint32_t H);
+uint64_t moe_down_partial_floats(uint32_t routes, uint32_t I, uint32_t H);   // plain plans' planes
 // Diagnostic: h[i] = SwiGLU(g[i], u[i]) with the block's activation arithmetic.
 hipError_t launch_moe_swiglu(const float* g, const float* u, float* h, uint64_t n, hipStream_t stream);
 

@@ -509,23 +509,27 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
                                               uint64_t active, int nrows, _Float16* act, float* red) {
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int jt = lane >> 3, g = lane & 7;
-    const uint32_t bps = a.bps_d, a0 = split * bps;
-    const uint32_t act_row = bps * 16;
+    // Blocks [a0, a0 + bps) of the input, inside 128-channel groups
+    // [g0, g0 + hblocks): the input stage covers whole groups (its Hadamard
+    // spans 128 channels) and the dot reads the split's blocks from `lead` on.
+    const uint32_t bps = a.bps_d, a0 = split * bps, g0 = a0 / 8, lead = a0 - 8 * g0;
+    const int hblocks = int(moe_down_groups(bps, split));
+    const uint32_t act_row = uint32_t(hblocks) * 128;
     constexpr uint32_t tb = 32u * K;
     const uint32_t rb = (a.I >> 4) * tb;
     const auto rs = make_rsrc(moe_first_ptr(ex.down.trellis) + uint64_t(a0) * rb, bps * rb);
     const uint32_t lo = (8u * c + jt) * tb + g * 4u * K;
-    const int nb = int(bps) / GEMV_WAVES;
+    const int nb = (int(bps) - w + GEMV_WAVES - 1) / GEMV_WAVES;   // blocks w, w + 4, ... of the split
     constexpr uint32_t kOut = 0x80000000u;
     auto off = [&](int t) -> uint32_t { return t < nb ? (w + GEMV_WAVES * t) * rb + lo : kOut; };
 
     // Input stage of the hidden rows; the first batch of units is loaded
     // ahead of the weight prefetch (see the gate/up core).
-    const int hblocks = int(bps) / 8, units = nrows * hblocks;
+    const int units = nrows * hblocks;
     auto unit_load = [&](int u) -> InputLoad {
         const int i = u / hblocks, hb = u - i * hblocks;
         const uint32_t j = moe_nth_route(active, i);
-        const uint32_t ch = a0 * 16 + hb * 128;
+        const uint32_t ch = (g0 + uint32_t(hb)) * 128;
         return input_load(a.hidden + uint64_t(j) * a.H + ch, ex.down.suh + ch, true);
     };
     auto unit_out = [&](int u) -> _Float16* { return act + (u / hblocks) * act_row + (u % hblocks) * 128; };
@@ -550,7 +554,7 @@ __device__ __forceinline__ void moe_down_core(const MoeArgs& a, const MoeExpert&
                 half2_t wq[4][4];
                 link_chunk(ring[u], first);
                 decode_chunk<K, CB_MUL1>(ring[u], wq);
-                mfma_dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
+                mfma_dot_block<RT>(wq, act + (lead + w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
             }
             load_chunk(ring[u], rs, off(t + u + MOE_RING_D));
         }

@@ -232,6 +232,17 @@ MoeSplit moe_split(uint32_t input, uint32_t max_bps) {
     return {bps, blocks / bps};
 }
 
+MoeSplit moe_split_staged(uint32_t H) {
+    const uint32_t blocks = H / 16;
+    if (blocks % 4 == 0) {
+        const uint32_t bps = blocks / 4;
+        bool fits = bps >= 1;
+        for (uint32_t s = 0; s < 4; ++s) fits = fits && moe_down_groups(bps, s) <= uint32_t(MOE_D_MAX_BPS) / 8;
+        if (fits) return {bps, 4};
+    }
+    return moe_split(H, MOE_D_MAX_BPS);
+}
+
 uint64_t moe_gate_up_partial_floats(uint32_t routes, uint32_t I, uint32_t H) {
     return uint64_t(routes) * moe_split(I, MOE_GU_MAX_BPS).splits * 2 * H;
 }

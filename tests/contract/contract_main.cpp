@@ -597,7 +597,7 @@ static void moe_plan(strix_context c, hipStream_t hs) {
     uint64_t split_need = 0;
     STATUS(strix_tp_moe_split_workspace_bytes(c, &d, &split_need), STRIX_SUCCESS);
     const uint64_t hidden_bytes = uint64_t(rows) * k * H * 4;
-    const uint32_t sd = stx::moe_split(H, stx::MOE_D_MAX_BPS).splits;
+    const uint32_t sd = stx::moe_split_staged(H).splits;
     CHECK(split_need == ((hidden_bytes + 255) & ~uint64_t(255)) + uint64_t(rows) * k * sd * I * 4);
     STATUS(strix_tp_moe_plan_create_split(c, &d, &st, &p), STRIX_ERROR_INSUFFICIENT_BUFFER);   // hidden only
     CHECK(p == nullptr && fake::live.size() == live0);
@@ -801,6 +801,15 @@ static void policy_rules() {
             const stx::MoeSplit ms = stx::moe_split(input, max_bps);
             CHECK(ms.bps % 8 == 0 && ms.bps >= 8 && ms.bps <= max_bps && uint64_t(ms.bps) * ms.splits * 16 == input);
         }
+    // Split plans' down: the reference's four equal parts up to H = 5120, and
+    // every part's 128-channel groups within the down kernel's LDS.
+    for (uint32_t H = 128; H <= 16384; H += 128) {
+        const stx::MoeSplit ms = stx::moe_split_staged(H);
+        CHECK(uint64_t(ms.bps) * ms.splits * 16 == H);
+        if (H <= 5120) CHECK(ms.splits == 4);
+        for (uint32_t s = 0; s < ms.splits; ++s) CHECK(stx::moe_down_groups(ms.bps, s) <= uint32_t(stx::MOE_D_MAX_BPS) / 8);
+    }
+    CHECK(stx::moe_split_staged(1152).bps == 18 && stx::moe_down_groups(18, 1) == 3 && stx::moe_down_groups(18, 3) == 3);
 }
 
 // Allocation-free GEMV: no allocation, free, copy or synchronisation; the

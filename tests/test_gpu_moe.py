@@ -259,7 +259,8 @@ def _same_bits(a, b):
 
 def test_split_plan_checkpoints(ctx):
     """Split plans keep the down core's per-split partials P [rows, k, S, I] in
-    the workspace.  The fused down and the staged core write the same P; the
+    the workspace (S = 4 here, the reference's partition; the plain plan's
+    own split count differs).  The fused down and the staged core write the same P; the
     route-alone core writes it again without the expert grouping; the staged
     finish reproduces the fused output from P and, on any P, the oracle's
     finish bit for bit; P's split sums meet the core's FP64 bound.  Plain plans
@@ -283,13 +284,18 @@ def test_split_plan_checkpoints(ctx):
     plan = runtime.MoePlan(ctx, ws, _dev(x), y, device_ids=_dev(ids.astype(np.int32)), device_scores=_dev(sc),
                            split=True)
     S = plan.partials.shape[2]
-    assert plan.partials.shape == (R, k, S, I) and S >= 2
+    assert plan.partials.shape == (R, k, S, I) and S == 4
     plan.submit()
     torch.cuda.synchronize()
     y_full, P_full = y.cpu().numpy(), plan.partials.cpu().numpy()
     hidden = plan.hidden.cpu().numpy()
-    assert _same_bits(y_full, y_plain)
     assert np.isfinite(P_full[routed]).all()
+    # the fused split output is the oracle's finish of its own planes; the
+    # plain plan folds the down core in another split count, so it agrees
+    # within the reference GPU gate, NaN row included
+    assert _same_bits(y_full, moe.down_finish(P_full, bank, ids, sc))
+    assert np.isnan(y_full[2]).all()
+    synth.gate(y_full[:2], y_plain[:2].astype(np.float64))
 
     # the staged core writes the same P for every computed route, nothing else
     plan.partials.fill_(float("nan"))
@@ -359,6 +365,68 @@ def test_split_plan_checkpoints(ctx):
     pp.destroy()
     _destroy(ws)
 
+
+
+def test_split_plan_reference_partition(ctx):
+    """At the reference's split geometry (5120 <-> 1152, top-6) a split plan's
+    P is [rows, 6, 4, 5120], split u over the down input's blocks
+    [18 u, 18 u + 18) (reference src/tp_fused_layout.hpp:19-24): each plane
+    meets the FP64 bound of the core over its own 288 channels alone, so a
+    shifted or resized partition fails.  Split u = 1 and 3 start inside a
+    128-channel group.  The staged finish of reference-layout planes follows
+    the oracle's finish bit for bit, and the fused output equals the plain
+    plan's up to the fold order (planes vs. one sum)."""
+    from oracle import codec, linear
+    E, I, H, R, k = 8, 5120, 1152, 2, 6
+    print(f"moe split plan reference partition E={E} I={I} H={H} R={R} k={k}", flush=True)
+    bank = synth.moe_bank(E, I, H, 2, 731, bias=True)
+    ws = _weights(ctx, bank)
+    ids, sc = synth.routes(R, E, k, 732)
+    x = synth.activations(R, I, 733)
+    y = torch.full((R, I), float("nan"), device=DEV)
+    plan = runtime.MoePlan(ctx, ws, _dev(x), y, device_ids=_dev(ids.astype(np.int32)), device_scores=_dev(sc),
+                           split=True)
+    assert plan.partials.shape == (R, k, 4, I)
+    plan.submit()
+    torch.cuda.synchronize()
+    y_full, P = y.cpu().numpy(), plan.partials.cpu().numpy()
+    hidden = plan.hidden.cpu().numpy()
+    assert np.isfinite(P).all() and np.isfinite(y_full).all()
+    # the staged core writes the same planes
+    plan.partials.fill_(float("nan"))
+    plan.down_core()
+    torch.cuda.synchronize()
+    assert _same_bits(plan.partials.cpu().numpy(), P)
+
+    qs = {}
+    for r in range(R):
+        for s in range(k):
+            e = int(ids[r, s])
+            tr, suh, _, _, kk = bank[e]["down"]
+            if e not in qs:
+                qs[e] = codec.dequantize_rotated(tr, kk)
+            a = linear.input_stages_fp32(hidden[r, s][None, :], suh)["core_input_fp16"]
+            for u in range(4):
+                c0, c1 = 288 * u, 288 * (u + 1)
+                exact = linear.core_exact_f64(a[:, c0:c1], qs[e][c0:c1])[0]
+                bound = linear.gamma_bound(a[:, c0:c1], qs[e][c0:c1])[0]
+                assert np.all(np.abs(P[r, s, u] - exact) <= bound), (r, s, u)
+    # the finish from the planes as they are is the oracle's finish
+    assert _same_bits(y_full, moe.down_finish(P, bank, ids, sc))
+    g = synth.rng(734)
+    Q = (g.standard_normal((R, k, 4, I)) * 50).astype(np.float32)
+    plan.partials.copy_(_dev(Q))
+    y.fill_(0.0)
+    plan.down_finish()
+    torch.cuda.synchronize()
+    assert _same_bits(y.cpu().numpy(), moe.down_finish(Q, bank, ids, sc))
+    plan.destroy()
+    # against the plain plan (one down sum): the same hidden, outputs within
+    # the reference GPU gate of each other
+    y_plain, h_plain = _run(ctx, ws, x, ids, sc, device=True)
+    assert _same_bits(h_plain, hidden)
+    synth.gate(y_full, y_plain.astype(np.float64))
+    _destroy(ws)
 
 def test_down_finish_slot_order_fixed_by_arithmetic(ctx):
     """The device's slot combine is ascending from +0, pinned by arithmetic
