@@ -477,6 +477,13 @@ constexpr int gemv_waves_per_eu() { return (RT == 8 && K >= 6) || (RT == 6 && K 
 // needed later.  Same bits; with nothing else read from memory ahead of the
 // first loads (below) measured 3.8 % faster on C1 (7.20 -> 6.93 us) and 1-4 %
 // on 4096 -> 12288 and 5120^2 at R1-R8.
+// Weight blocks in flight per wave.  Fewer than four left the later
+// workgroups of a CU less to wait behind (their input loads queue after the
+// earlier workgroups' rings): interleaved A/B, same bits, 4 -> 3 measured
+// 2-5 % faster on 4096 -> 12288 at K4-K6 R1-R8, up to 4 % on 5120^2, C1 and
+// grouped o_a unchanged; 6 and 8 were slower everywhere, 2 mixed.
+constexpr int kGemvRing = 3;
+
 template <int K, int CB, int RT>
 __global__ __launch_bounds__(GEMV_THREADS) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu<K, RT>())))
 void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, uint32_t* epochs,
@@ -537,10 +544,10 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     _Float16* act = reinterpret_cast<_Float16*>(smem);                  // [RT][bps*16]
     float* red = reinterpret_cast<float*>(smem + RT * act_row * 2);       // [4][RT][128]
 
-    // Prefetch ring of depth 4.  Loads are issued unconditionally so the
-    // compiler can count them exactly (vmcnt(3) per use); past the last block
-    // the offset is out of the buffer's range, which the hardware answers
-    // with zeros and no memory access.
+    // Prefetch ring of kGemvRing blocks per wave.  Loads are issued
+    // unconditionally so the compiler can count them exactly; past the last
+    // block the offset is out of the buffer's range, which the hardware
+    // answers with zeros and no memory access.
     constexpr uint32_t kOutOfRange = 0x80000000u;
     auto block_off = [&](int t) -> uint32_t {
         return t < nb ? (w + GEMV_WAVES * t) * row_bytes + lane_off : kOutOfRange;
@@ -598,7 +605,7 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     // ring, then the rest only once their own input has arrived (4096^2 K4 R1:
     // 7.53 -> 7.32 us; the whole ring after the input: 7.46 us).  With three or
     // more rounds the wait measured 1-3 % slower, so it is not taken.
-    Chunk<K> ring[4];
+    Chunk<K> ring[kGemvRing];
     load_chunk(ring[0], rsrc, block_off(0));
     __builtin_amdgcn_sched_barrier(0);
     if (blockIdx.x < first_round_end) {
@@ -608,7 +615,7 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 1; u < 4; ++u) load_chunk(ring[u], rsrc, block_off(u));
+    for (int u = 1; u < kGemvRing; ++u) load_chunk(ring[u], rsrc, block_off(u));
 
     // The chunks stay in their registers across the input stage: decoding
     // blocks ahead of the barrier (to overlap the input loads) was measured
@@ -624,10 +631,10 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     const bool first = g == 0;
     MfmaAcc<RT> acc;
     mfma_acc_zero(acc);
-    // Slot t % 4 holds block t; it is refilled with block t + 4.
-    for (int t = 0; t < nb; t += 4) {
+    // Slot t % kGemvRing holds block t; it is refilled with block t + kGemvRing.
+    for (int t = 0; t < nb; t += kGemvRing) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kGemvRing; ++u) {
             Chunk<K>& slot = ring[u];
             if (t + u < nb) {
                 half2_t wq[4][4];
@@ -635,7 +642,7 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
                 decode_chunk<K, CB>(slot, wq);
                 mfma_dot_block<RT>(wq, act + (w + GEMV_WAVES * (t + u)) * 16, act_row, acc);
             }
-            load_chunk(slot, rsrc, block_off(t + u + 4));
+            load_chunk(slot, rsrc, block_off(t + u + kGemvRing));
         }
     }
 
