@@ -488,6 +488,61 @@ static void direct_calls(strix_context c, hipStream_t hs) {
 
 // Routed-expert plan over host routes: creation failures leave nothing
 // behind, submission is quiet, and invalid routes are rejected up front.
+// The reference's split geometry (5120 <-> 1152, top-6; reference
+// src/tp_moe_split_layout.hpp:29-34): the workspace queries give its byte
+// counts for 1-8 rows, hidden [rows][6][1152] F32 = rows x 27,648 bytes, then
+// P [rows][6][4][5120] F32 = rows x 491,520 bytes with no padding between.
+static void moe_reference_split_geometry(strix_context c, hipStream_t hs) {
+    const uint32_t I = 5120, H = 1152, k = 6, experts = 6;
+    strix_stream st = stream_of(hs);
+    std::vector<HostLinear> host;
+    for (uint32_t e = 0; e < experts; ++e) {
+        host.emplace_back(H, I, 2, false);
+        host.emplace_back(H, I, 2, false);
+        host.emplace_back(I, H, 2, false);
+    }
+    std::vector<strix_weights> ws(host.size());
+    for (size_t i = 0; i < host.size(); ++i) {
+        const strix_exl3_parts_desc p = host[i].parts();
+        STATUS(strix_weights_prepare_parts(c, &p, &st, &ws[i]), STRIX_SUCCESS);
+    }
+    std::vector<strix_tp_expert_desc> ex(experts);
+    for (uint32_t e = 0; e < experts; ++e) {
+        ex[e] = header<strix_tp_expert_desc>();
+        ex[e].expert_id = e;
+        ex[e].gate = ws[3 * e];
+        ex[e].up = ws[3 * e + 1];
+        ex[e].down = ws[3 * e + 2];
+    }
+    CHECK(stx::moe_split_staged(H).bps == 18 && stx::moe_split_staged(H).splits == 4);
+    for (uint32_t rows = 1; rows <= 8; ++rows) {
+        void* x = device_alloc(rows * I * 4);
+        void* y = device_alloc(rows * I * 4);
+        std::vector<uint32_t> ids(rows * k);
+        std::vector<float> scores(rows * k, 1.0f / 6);
+        for (uint32_t r = 0; r < rows; ++r)
+            for (uint32_t q = 0; q < k; ++q) ids[r * k + q] = (r + q) % experts;
+        strix_tp_moe_desc d;
+        strix_tp_moe_desc_init(&d);
+        d.input = tensor(x, rows * I * 4, rows, I, 2);
+        d.output = tensor(y, rows * I * 4, rows, I, 2);
+        d.experts = ex.data();
+        d.expert_count = experts;
+        d.route_ids = ids.data();
+        d.route_ids_count = rows * k;
+        d.route_scores = scores.data();
+        d.route_scores_count = rows * k;
+        uint64_t plain = 0, split = 0;
+        STATUS(strix_tp_moe_workspace_bytes(c, &d, &plain), STRIX_SUCCESS);
+        STATUS(strix_tp_moe_split_workspace_bytes(c, &d, &split), STRIX_SUCCESS);
+        CHECK(plain == uint64_t(rows) * 27648);
+        CHECK(split == uint64_t(rows) * 27648 + uint64_t(rows) * 491520);
+        CHECK(hipFree(x) == hipSuccess);
+        CHECK(hipFree(y) == hipSuccess);
+    }
+    for (strix_weights w : ws) STATUS(strix_weights_destroy(w), STRIX_SUCCESS);
+}
+
 static void moe_plan(strix_context c, hipStream_t hs) {
     const uint32_t I = 256, H = 512, rows = 2, k = 2, experts = 3;
     strix_stream st = stream_of(hs);
@@ -921,6 +976,7 @@ int main() {
     prepare_failures(c, hs);
     direct_calls(c, hs);
     moe_plan(c, hs);
+    moe_reference_split_geometry(c, hs);
     noalloc_calls(c, hs);
     stream_read_calls(c, hs);
     // The default stream (NULL) is accepted everywhere a stream is.
