@@ -380,6 +380,137 @@ __device__ __forceinline__ void finish_polled(const GemvArgs& a, const GroupWeig
     }
 }
 
+// Five to eight rows: plane words in quads.  Each 32-lane half of a wave
+// holds one row, lane l = lane & 31 its columns 4l .. 4l + 3, so one 16-byte
+// access carries what two 8-byte ones do in the pair layout: a finisher wave
+// then polls each other split's words of its two rows with one load per lane,
+// where the pair layout takes two (at two rows per wave the poll round is
+// bound by the loads in flight, not by their bytes).
+typedef float gemv_q_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ gemv_q_t poll_quad(__amdgpu_buffer_rsrc_t planes, uint32_t voffset, uint32_t soffset) {
+    return __builtin_bit_cast(gemv_q_t, __builtin_amdgcn_raw_buffer_load_b128(planes, voffset, soffset, kCoherentAux));
+}
+__device__ __forceinline__ bool filled(gemv_q_t v) {
+    return __builtin_bit_cast(uint32_t, v.x) != GEMV_PLANE_EMPTY && __builtin_bit_cast(uint32_t, v.y) != GEMV_PLANE_EMPTY &&
+           __builtin_bit_cast(uint32_t, v.z) != GEMV_PLANE_EMPTY && __builtin_bit_cast(uint32_t, v.w) != GEMV_PLANE_EMPTY;
+}
+
+// One poll round of NB quad loads per lane at soffset (first + u) * stride
+// (u < count, the rest out of range): polls until every word has arrived or
+// the limit runs out (false); then adds load u to z for u < count in
+// ascending u.
+template <int NB>
+__device__ __forceinline__ bool poll_fold_quads(gemv_q_t& z, __amdgpu_buffer_rsrc_t planes, uint32_t voff,
+                                                uint32_t first, uint32_t stride, int count, uint32_t limit) {
+    gemv_q_t v[NB];
+    for (uint32_t spin = 0;; ++spin) {
+        asm volatile("" ::: "memory");
+        const int cnt = int(step_offset(uint32_t(count)));
+        uint32_t so = step_offset(stride) * first;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            v[u] = poll_quad(planes, u < cnt ? voff : kPollOutOfRange, so);
+            so += stride;
+        }
+        bool ready = true;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) ready &= filled(v[u]);
+        if (__all(ready)) break;
+        if (spin + 1 >= limit) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const gemv_q_t t = z + v[u];
+        z = u < count ? t : z;
+    }
+    return true;
+}
+
+// H32 of one row held as quads over a 32-lane half: element strides 1 and 2
+// inside the lane, 4 .. 64 across lanes 1 .. 16 apart.  Each level combines
+// the same element pairs with the same operations (lower + upper,
+// lower - upper, one FP32 rounding each) as h32_wave, so the same bits.
+__device__ __forceinline__ void h32_quads(gemv_q_t& z) {
+    const float a0 = z.x + z.y, a1 = z.x - z.y, a2 = z.z + z.w, a3 = z.z - z.w;
+    float v0 = a0 + a2, v2 = a0 - a2, v1 = a1 + a3, v3 = a1 - a3;
+    auto stage = [&](auto st) {
+        constexpr int S = decltype(st)::value;
+        butterfly<S>(v0, v1);
+        butterfly<S>(v2, v3);
+    };
+    stage(std::integral_constant<int, 1>{});
+    stage(std::integral_constant<int, 2>{});
+    stage(std::integral_constant<int, 4>{});
+    stage(std::integral_constant<int, 8>{});
+    stage(std::integral_constant<int, 16>{});
+    z.x = rn32(v0 * INV_SQRT128);
+    z.y = rn32(v1 * INV_SQRT128);
+    z.z = rn32(v2 * INV_SQRT128);
+    z.w = rn32(v3 * INV_SQRT128);
+}
+
+// Finisher of a single launch at five to eight rows (finish_polled's
+// protocol and fold order, quads instead of pairs): wave w finishes rows w
+// and w + 4 (lanes 0-31 and 32-63), up to kQuadPolls other splits per round
+// (16-byte loads: the registers of a pair round's 8-byte ones).
+constexpr int kQuadPolls = kPollLoads / 2;
+template <int RT>
+__device__ __forceinline__ void finish_polled_wide(const GemvArgs& a, const GroupWeights& gw, float* y, int c,
+                                                   const float* red, uint32_t* flag, const float* cur, uint32_t epoch,
+                                                   uint32_t cz) {
+    static_assert(RT > GEMV_WAVES && RT <= 2 * GEMV_WAVES, "two rows per wave");
+    const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)), lane = threadIdx.x & 63, l = lane & 31;
+    const uint32_t r = uint32_t(w + GEMV_WAVES * (lane >> 5));   // rows >= 5: every wave has row w
+    const bool live = r < a.rows;
+    const int others = int(a.splits) - 1;
+    const uint32_t stride = a.rows * 512u;   // one split's [rows][128] F32
+    const auto planes = make_rsrc(cur, uint32_t(others) * stride);
+    const uint32_t limit = a.poll_limit, voff = live ? r * 512u + uint32_t(l) * 16u : kPollOutOfRange;
+    // Output-stage operands of columns 128c + 4l .. +3 (in flight during the polls).
+    const uint32_t n0 = 128u * uint32_t(c) + 4u * uint32_t(l);
+    const u32x2 svq = ld_global(reinterpret_cast<const u32x2*>(gw.svh + n0));
+    const auto rb = make_rsrc(gw.bias, gw.bias ? a.N * 4u : 0u);
+    const gemv_q_t bias = __builtin_bit_cast(gemv_q_t, __builtin_amdgcn_raw_buffer_load_b128(rb, n0 * 4u, 0, 0));
+    gemv_q_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+    bool complete = limit != 0 && !(epoch & GEMV_EPOCH_POISON);
+    for (int s0 = 0; s0 < others && complete;) {
+        const int count = others - s0 < kQuadPolls ? others - s0 : kQuadPolls;
+        if (count <= 8)
+            complete = poll_fold_quads<8>(z, planes, voff, uint32_t(s0), stride, count, limit);
+        else
+            complete = poll_fold_quads<kQuadPolls>(z, planes, voff, uint32_t(s0), stride, count, limit);
+        s0 += count;
+    }
+    const uint32_t rr = live ? r : uint32_t(w);
+    const gemv_q_t own = *reinterpret_cast<const gemv_q_t*>(red + rr * 128 + 4 * l);
+    const float nan = __builtin_nanf("");
+    z = complete ? z + own : gemv_q_t{nan, nan, nan, nan};
+    if (!complete) *flag = 1u;
+    h32_quads(z);
+    if (live) {
+        const uint16_t sv[4] = {uint16_t(svq.x), uint16_t(svq.x >> 16), uint16_t(svq.y), uint16_t(svq.y >> 16)};
+        float* yr = y + r * a.y_row_stride + n0;
+        const bool hb = gw.bias != nullptr;
+        gemv_f2_t o0, o1;
+        o0.x = output_value(z.x, sv[0], hb, bias.x, a.alpha, a.beta, yr);
+        o0.y = output_value(z.y, sv[1], hb, bias.y, a.alpha, a.beta, yr + 1);
+        o1.x = output_value(z.z, sv[2], hb, bias.z, a.alpha, a.beta, yr + 2);
+        o1.y = output_value(z.w, sv[3], hb, bias.w, a.alpha, a.beta, yr + 3);
+        *(__attribute__((address_space(1))) gemv_f2_t*)(yr) = o0;
+        *(__attribute__((address_space(1))) gemv_f2_t*)(yr + 2) = o1;
+    }
+    // Every wave's verdict is in `flag`: advance the epoch, or poison it.
+    lds_barrier();
+    if (threadIdx.x == 0) {
+        const bool gave_up = *flag != 0u;
+        if (gave_up)
+            __hip_atomic_fetch_or(a.state.status, GEMV_STATUS_GAVE_UP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t next = gave_up ? (epoch | GEMV_EPOCH_POISON) : ((epoch + 1u) & ~GEMV_EPOCH_POISON);
+        __hip_atomic_store(a.state.epochs + cz, next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Matrix-core dot: v_mfma_f32_4x4x4_16b_f16, sixteen 4x4x4 products per
 // instruction.  Operand layout, checked on the device: block b uses lanes
@@ -653,21 +784,50 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     float* cur = fused ? fused_planes(a, place.cz, epoch & 1u) : nullptr;
     float* prev = fused ? fused_planes(a, place.cz, (epoch & 1u) ^ 1u) : nullptr;
     float* plane_base = a.partials + (uint64_t(z) * a.splits) * a.rows * a.N;
-    for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
-        const int r = idx >> 7, n = idx & 127;
-        float v = red[(0 * RT + r) * 128 + n];
+    if constexpr (RT > GEMV_WAVES) {
+        // Five to eight rows: a quad of columns per thread, 16-byte LDS reads
+        // and plane stores (the same element-wise adds in wave order); the
+        // single-launch words go out with the sc1 policy, as store_coherent's.
+        const uint32_t set_bytes = (a.splits - 1) * a.rows * 512u;
+        const auto cur_rs = make_rsrc(cur, fused ? set_bytes : 0u);
+        const auto prev_rs = make_rsrc(prev, fused ? set_bytes : 0u);
+        for (int q = tid; q < RT * 32; q += GEMV_THREADS) {
+            const int r = q >> 5, n = (q & 31) * 4;
+            gemv_q_t v = *reinterpret_cast<const gemv_q_t*>(red + (0 * RT + r) * 128 + n);
 #pragma unroll
-        for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + red[(ww * RT + r) * 128 + n];
-        if (finisher) {
-            red[r * 128 + n] = v;
-        } else if (uint32_t(r) < a.rows) {
-            if (fused) {
-                const uint64_t word = (uint64_t(s) * a.rows + r) * 128u + n;
-                store_coherent(cur + word, v);
-                store_coherent(prev + word, __builtin_bit_cast(float, GEMV_PLANE_EMPTY));
+            for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + *reinterpret_cast<const gemv_q_t*>(red + (ww * RT + r) * 128 + n);
+            if (finisher) {
+                *reinterpret_cast<gemv_q_t*>(red + r * 128 + n) = v;
+            } else if (uint32_t(r) < a.rows) {
+                if (fused) {
+                    const uint32_t off = ((uint32_t(s) * a.rows + uint32_t(r)) * 128u + uint32_t(n)) * 4u;
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), cur_rs, off, 0, kCoherentAux);
+                    __builtin_amdgcn_raw_buffer_store_b128(u32x4{GEMV_PLANE_EMPTY, GEMV_PLANE_EMPTY, GEMV_PLANE_EMPTY,
+                                                                 GEMV_PLANE_EMPTY},
+                                                           prev_rs, off, 0, kCoherentAux);
+                } else {
+                    *(__attribute__((address_space(1))) gemv_q_t*)(plane_base + (uint64_t(s) * a.rows + r) * a.N +
+                                                                  128 * c + n) = v;
+                }
             }
-            else
-                *(__attribute__((address_space(1))) float*)(plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c + n) = v;
+        }
+    } else {
+        for (int idx = tid; idx < RT * 128; idx += GEMV_THREADS) {
+            const int r = idx >> 7, n = idx & 127;
+            float v = red[(0 * RT + r) * 128 + n];
+#pragma unroll
+            for (int ww = 1; ww < GEMV_WAVES; ++ww) v = v + red[(ww * RT + r) * 128 + n];
+            if (finisher) {
+                red[r * 128 + n] = v;
+            } else if (uint32_t(r) < a.rows) {
+                if (fused) {
+                    const uint64_t word = (uint64_t(s) * a.rows + r) * 128u + n;
+                    store_coherent(cur + word, v);
+                    store_coherent(prev + word, __builtin_bit_cast(float, GEMV_PLANE_EMPTY));
+                }
+                else
+                    *(__attribute__((address_space(1))) float*)(plane_base + (uint64_t(s) * a.rows + r) * a.N + 128 * c + n) = v;
+            }
         }
     }
     if (!finisher) return;
@@ -685,7 +845,10 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
         return;
     }
     lds_barrier();
-    finish_polled<RT>(a, gw_finish(), y_of(), c, red, flag, cur, epoch, place.cz);
+    if constexpr (RT > GEMV_WAVES)
+        finish_polled_wide<RT>(a, gw_finish(), y_of(), c, red, flag, cur, epoch, place.cz);
+    else
+        finish_polled<RT>(a, gw_finish(), y_of(), c, red, flag, cur, epoch, place.cz);
 }
 
 // ---------------------------------------------------------------------------
