@@ -450,6 +450,36 @@ __device__ __forceinline__ void h32_quads(gemv_q_t& z) {
     z.w = rn32(v3 * INV_SQRT128);
 }
 
+// Input stage of one 128-channel unit per 32-lane half: lane l = lane & 31
+// loads x and suh of channels 4l .. 4l + 3 with one 16-byte and one 8-byte
+// load (a quarter of the load instructions of the (l, l + 64) layout), then
+// the same per-element arithmetic, H32 pairs and FP16 rounding.  x need only
+// be 4-byte aligned: ROCm runs compute queues in the unaligned memory-access
+// mode, where a multi-dword global load takes any dword-aligned address.
+struct InputQuad {
+    gemv_q_t x;
+    u32x2 u;
+};
+__device__ __forceinline__ InputQuad input_load_quad(const float* x, const uint16_t* suh, bool live) {
+    const int l = threadIdx.x & 31;
+    InputQuad q;
+    const gemv_q_t v = ld_global(reinterpret_cast<const gemv_q_t*>(x + 4 * l));
+    q.x = live ? v : gemv_q_t{0.0f, 0.0f, 0.0f, 0.0f};
+    q.u = ld_global(reinterpret_cast<const u32x2*>(suh + 4 * l));
+    return q;
+}
+__device__ __forceinline__ void input_compute_quad(const InputQuad& q, _Float16* out) {
+    const int l = threadIdx.x & 31;
+    gemv_q_t v;
+    v.x = (float)(_Float16)rn32(q.x.x * half_bits_to_float(uint16_t(q.u.x)));
+    v.y = (float)(_Float16)rn32(q.x.y * half_bits_to_float(uint16_t(q.u.x >> 16)));
+    v.z = (float)(_Float16)rn32(q.x.z * half_bits_to_float(uint16_t(q.u.y)));
+    v.w = (float)(_Float16)rn32(q.x.w * half_bits_to_float(uint16_t(q.u.y >> 16)));
+    h32_quads(v);
+    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<h4_t*>(out + 4 * l) = h4_t{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+}
+
 // Finisher of a single launch at five to eight rows (finish_polled's
 // protocol and fold order, quads instead of pairs): wave w finishes rows w
 // and w + 4 (lanes 0-31 and 32-63), up to kQuadPolls other splits per round
@@ -701,32 +731,52 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     // before the weight prefetch, so waiting for it does not wait for the
     // weights.  (Four units in flight make the 3- and 4-row mcg / 3inst
     // kernels spill, so those keep two.)
-    constexpr int kUnits = RT <= 2 ? 2 : RT <= 4 ? (CB == CB_MUL1 ? 4 : 2) : 8;
-    const int hblocks = a.bps / 8, units = RT * hblocks;
-    // Unit u is row u % RT of 128-block u / RT (constant divisors).
-    auto unit_load = [&](int u) -> InputLoad {
-        const int r = u % RT, hb = u / RT;
-        const uint32_t ch = a0 * 16 + hb * 128;
-        const bool live = uint32_t(r) < a.rows;
-        return input_load(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, live);
+    // The 8-row template's work item is a pair of units, one per 32-lane half
+    // (input_load_quad): 8 units per wave and batch in half the load
+    // instructions.  (Measured: 3-5 % faster at 7-8 rows; the same item at 5-6
+    // rows was up to 4 % slower, so the 6-row template keeps single units.)
+    constexpr bool kQuadIn = RT == 2 * GEMV_WAVES;
+    using Unit = std::conditional_t<kQuadIn, InputQuad, InputLoad>;
+    constexpr int kUnits = RT <= 2 ? 2 : RT <= 4 ? (CB == CB_MUL1 ? 4 : 2) : kQuadIn ? 4 : 8;
+    const int hblocks = a.bps / 8, units = kQuadIn ? RT * hblocks / 2 : RT * hblocks;
+    // Unit u is row u % RT of 128-block u / RT (constant divisors); a quad
+    // item v holds units 2v (lanes 0-31) and 2v + 1 (lanes 32-63).
+    auto unit_load = [&](int u) {
+        if constexpr (kQuadIn) {
+            const int uu = 2 * u + int(threadIdx.x >> 5 & 1), r = uu % RT, hb = uu / RT;
+            const uint32_t ch = a0 * 16 + hb * 128;
+            const bool live = uint32_t(r) < a.rows;
+            return input_load_quad(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, live);
+        } else {
+            const int r = u % RT, hb = u / RT;
+            const uint32_t ch = a0 * 16 + hb * 128;
+            const bool live = uint32_t(r) < a.rows;
+            return input_load(x + (live ? r * a.x_row_stride : 0) + ch, gw.suh + ch, live);
+        }
     };
-    auto unit_out = [&](int u) -> _Float16* { return act + (u % RT) * act_row + (u / RT) * 128; };
+    auto unit_out = [&](int u) -> _Float16* {
+        const int uu = kQuadIn ? 2 * u + int(threadIdx.x >> 5 & 1) : u;
+        return act + (uu % RT) * act_row + (uu / RT) * 128;
+    };
     // Units past the end load unit 0 again (valid addresses, result unused).
-    auto batch_load = [&](int u0, InputLoad (&l)[kUnits]) {
+    auto batch_load = [&](int u0, Unit (&l)[kUnits]) {
 #pragma unroll
         for (int i = 0; i < kUnits; ++i) {
             const int u = u0 + GEMV_WAVES * i;
             l[i] = unit_load(u < units ? u : 0);
         }
     };
-    auto batch_compute = [&](int u0, const InputLoad (&l)[kUnits]) {
+    auto batch_compute = [&](int u0, const Unit (&l)[kUnits]) {
 #pragma unroll
         for (int i = 0; i < kUnits; ++i) {
             const int u = u0 + GEMV_WAVES * i;
-            if (u < units) input_compute(l[i], unit_out(u));
+            if (u < units) {
+                if constexpr (kQuadIn) input_compute_quad(l[i], unit_out(u));
+                else input_compute(l[i], unit_out(u));
+            }
         }
     };
-    InputLoad pre[kUnits];
+    Unit pre[kUnits];
     batch_load(w, pre);
     __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the weight prefetch
     // A grid of two dispatch rounds (257..512 workgroups on 256 CUs, the
@@ -753,7 +803,7 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     // slower, the decoded weights holding 32 more VGPRs per lane.
     batch_compute(w, pre);
     for (int u0 = w + kUnits * GEMV_WAVES; u0 < units; u0 += kUnits * GEMV_WAVES) {
-        InputLoad l[kUnits];
+        Unit l[kUnits];
         batch_load(u0, l);
         batch_compute(u0, l);
     }
