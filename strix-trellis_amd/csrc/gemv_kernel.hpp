@@ -731,13 +731,14 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     // before the weight prefetch, so waiting for it does not wait for the
     // weights.  (Four units in flight make the 3- and 4-row mcg / 3inst
     // kernels spill, so those keep two.)
-    // The 8-row template's work item is a pair of units, one per 32-lane half
-    // (input_load_quad): 8 units per wave and batch in half the load
-    // instructions.  (Measured: 3-5 % faster at 7-8 rows; the same item at 5-6
-    // rows was up to 4 % slower, so the 6-row template keeps single units.)
-    constexpr bool kQuadIn = RT == 2 * GEMV_WAVES;
+    // The 2- and 8-row templates' work item is a pair of units, one per
+    // 32-lane half (input_load_quad): the same units per wave and batch from a
+    // quarter of the load instructions.  (Measured: 3-5 % faster at 7-8 rows
+    // and up to 5.6 % at 2 rows; the same item was up to 4 % slower at 5-6
+    // rows and mixed at 3-4, so those templates keep single units.)
+    constexpr bool kQuadIn = RT == 2 * GEMV_WAVES || RT == 2;
     using Unit = std::conditional_t<kQuadIn, InputQuad, InputLoad>;
-    constexpr int kUnits = RT <= 2 ? 2 : RT <= 4 ? (CB == CB_MUL1 ? 4 : 2) : kQuadIn ? 4 : 8;
+    constexpr int kUnits = (RT <= 2 ? 2 : RT <= 4 ? (CB == CB_MUL1 ? 4 : 2) : 8) / (kQuadIn ? 2 : 1);
     const int hblocks = a.bps / 8, units = kQuadIn ? RT * hblocks / 2 : RT * hblocks;
     // Unit u is row u % RT of 128-block u / RT (constant divisors); a quad
     // item v holds units 2v (lanes 0-31) and 2v + 1 (lanes 32-63).

@@ -188,14 +188,14 @@ def test_rows_plans_and_entry_points_bit_identical(ctx, I, N, K):
         assert torch.equal(yp.view(torch.int32), y8.view(torch.int32))
     assert plan.launches() == 1
     plan.destroy()
-    # 3 rows (3-row template), 5 or 6 rows (6-row template) and 7 rows (8-row
-    # template, one dead row) keep their bits
-    for rows in (3, 5, 6, 7):
+    # 2 rows (2-row template), 3 rows (3-row template), 5 or 6 rows (6-row
+    # template) and 7 rows (8-row template, one dead row) keep their bits
+    for rows in (2, 3, 5, 6, 7):
         yr = torch.empty((rows, N), device=DEV)
         runtime.gemv(w, x[:rows].contiguous(), yr)
         assert torch.equal(yr.view(torch.int32), y8[:rows].view(torch.int32)), rows
     # x only 4-byte aligned, which is all the ABI asks of it: the same bits
-    for rows in (8, 6, 1):
+    for rows in (8, 6, 2, 1):
         buf = torch.empty(rows * I + 1, device=DEV)
         xm = buf[1:].view(rows, I)
         xm.copy_(x[:rows])
