@@ -5,10 +5,15 @@
 
 namespace stx {
 
-// Row template of a call: rows are computed in groups of 1, 2, 3, 4, 6 or 8
+// Row template of a call: rows are computed in groups of 1, 2, 3, 4 or 8
 // (the rows past the call's are zero inputs whose results are never stored).
-// A row's arithmetic does not depend on the template.
-static uint32_t rows_template(uint64_t rows) { return rows <= 4 ? uint32_t(rows ? rows : 1) : rows <= 6 ? 6 : 8; }
+// A row's arithmetic does not depend on the template.  Five and six rows run
+// the 8-row template: measured 0.4-2.9 % faster than a 6-row one on C1, C4
+// and the 5120^2 / 4096 -> 12288 layers (one cell +0.1 %).  The owner-fold
+// kernel keeps a 6-row template (its 8-row instance: 42.2-42.5 us at 7-8 rows
+// of 16 x 4096 -> 1024 K5 against 40.1 us for the 6-row one at 5-6).
+static uint32_t rows_template(uint64_t rows) { return rows <= 4 ? uint32_t(rows ? rows : 1) : 8; }
+static uint32_t owner_rows_template(uint64_t rows) { return rows <= 6 && rows > 4 ? 6 : rows_template(rows); }
 
 using GemvDispatch = hipError_t (*)(const GemvLaunch&);
 static const GemvDispatch gemv_table[8] = {gemv_dispatch<1>, gemv_dispatch<2>, gemv_dispatch<3>,
@@ -183,7 +188,7 @@ static const GemvOwnerDispatch owner_table[8] = {gemv_owner_dispatch<1>, gemv_ow
 // The owner kernel keeps its inputs and wave partials in at most 64 KiB of LDS.
 bool gemv_owner_fits(const DeviceWeights& w, uint64_t rows) {
     const GemvShape sh = gemv_shape(w.input, w.output, w.bits);
-    return rows >= 1 && rows <= 8 && sh.splits > 1 && owner_lds_bytes(rows_template(rows), sh.bps) <= 65536;
+    return rows >= 1 && rows <= 8 && sh.splits > 1 && owner_lds_bytes(owner_rows_template(rows), sh.bps) <= 65536;
 }
 
 hipError_t launch_gemv_owner(const DeviceWeights& geometry, const GroupWeights* table, uint32_t groups,
@@ -193,6 +198,7 @@ hipError_t launch_gemv_owner(const DeviceWeights& geometry, const GroupWeights* 
     GemvLaunch l = make_launch(geometry, table, groups, call, x_group_stride, y_group_stride, nullptr, nullptr,
                                stream);
     l.grid = dim3(l.args.ncg * groups, 1, 1);
+    l.rows_template = owner_rows_template(call.rows);
     l.lds = owner_lds_bytes(l.rows_template, l.args.bps);
     return owner_table[geometry.bits - 1](l);
 }

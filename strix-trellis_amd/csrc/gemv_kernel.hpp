@@ -624,10 +624,10 @@ __device__ __forceinline__ void mfma_partials(const MfmaAcc<RT>& acc, float* red
 
 // Register budget: five waves per SIMD (<= 96 VGPRs), measured faster than
 // four (C1 8.9 -> 8.3 us; 16 x 4096 -> 1024 R4 32.5 -> 30.4 us) even where the
-// grid is smaller than one resident round.  The 8-row K >= 6 and 6-row K8
-// instances would spill at that budget and keep four.
+// grid is smaller than one resident round.  The 8-row K >= 6 instances would
+// spill at that budget and keep four.
 template <int K, int RT>
-constexpr int gemv_waves_per_eu() { return (RT == 8 && K >= 6) || (RT == 6 && K == 8) ? 4 : 5; }
+constexpr int gemv_waves_per_eu() { return RT == 8 && K >= 6 ? 4 : 5; }
 
 // The fields every workgroup needs before its first memory access come as
 // scalar arguments ahead of GemvArgs (16-bit pairs where the values fit), so
@@ -734,8 +734,7 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     // The 2- and 8-row templates' work item is a pair of units, one per
     // 32-lane half (input_load_quad): the same units per wave and batch from a
     // quarter of the load instructions.  (Measured: 3-5 % faster at 7-8 rows
-    // and up to 5.6 % at 2 rows; the same item was up to 4 % slower at 5-6
-    // rows and mixed at 3-4, so those templates keep single units.)
+    // and up to 5.6 % at 2 rows; mixed at 3-4 rows, where single units stay.)
     constexpr bool kQuadIn = RT == 2 * GEMV_WAVES || RT == 2;
     using Unit = std::conditional_t<kQuadIn, InputQuad, InputLoad>;
     constexpr int kUnits = (RT <= 2 ? 2 : RT <= 4 ? (CB == CB_MUL1 ? 4 : 2) : 8) / (kQuadIn ? 2 : 1);
@@ -1063,7 +1062,7 @@ __global__ __launch_bounds__(64) void decode_kernel(const uint32_t* trellis, uin
 struct GemvLaunch {
     GemvArgs args;
     dim3 grid;
-    uint32_t rows_template;   // 1, 2, 3, 4, 6 or 8
+    uint32_t rows_template;   // 1, 2, 3, 4 or 8 (the owner-fold kernel also 6)
     uint32_t codebook;
     size_t lds;
     hipStream_t stream;
@@ -1083,15 +1082,16 @@ hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t 
     hipError_t gemv_dispatch<K>(const GemvLaunch& l) {                                                    \
         using Fn = void (*)(const uint32_t*, const uint16_t*, const float*, uint32_t*, const GroupWeights*,  \
                             uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, GemvArgs);                   \
-        static const Fn table[3][6] = {                                                                   \
+        static const Fn table[3][5] = {                                                                   \
             {gemv_kernel<K, 0, 1>, gemv_kernel<K, 0, 2>, gemv_kernel<K, 0, 3>, gemv_kernel<K, 0, 4>,      \
-             gemv_kernel<K, 0, 6>, gemv_kernel<K, 0, 8>},                                                 \
+             gemv_kernel<K, 0, 8>},                                                                       \
             {gemv_kernel<K, 1, 1>, gemv_kernel<K, 1, 2>, gemv_kernel<K, 1, 3>, gemv_kernel<K, 1, 4>,      \
-             gemv_kernel<K, 1, 6>, gemv_kernel<K, 1, 8>},                                                 \
+             gemv_kernel<K, 1, 8>},                                                                       \
             {gemv_kernel<K, 2, 1>, gemv_kernel<K, 2, 2>, gemv_kernel<K, 2, 3>, gemv_kernel<K, 2, 4>,      \
-             gemv_kernel<K, 2, 6>, gemv_kernel<K, 2, 8>}};                                                \
+             gemv_kernel<K, 2, 8>}};                                                                      \
         const int rt = int(l.rows_template);                                                              \
-        const int ri = rt <= 4 ? rt - 1 : rt == 6 ? 4 : 5;                                                \
+        if (rt != 8 && (rt < 1 || rt > 4)) return hipErrorInvalidValue;                                  \
+        const int ri = rt <= 4 ? rt - 1 : 4;                                                              \
         const GemvArgs& a = l.args;                                                                       \
         if (a.ncg > 0xFFFFu || a.groups > 0xFFFFu || a.bps > 0xFFFFu || a.splits > 0xFFFFu ||             \
             a.rows > 0xFFu || a.mode > 0xFFu || a.x_row_stride > 0xFFFFFFFFull)                           \
