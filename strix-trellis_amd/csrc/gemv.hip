@@ -5,15 +5,18 @@
 
 namespace stx {
 
-// Row template of a call: rows are computed in groups of 1, 2, 3, 4 or 8
-// (the rows past the call's are zero inputs whose results are never stored).
-// A row's arithmetic does not depend on the template.  Five and six rows run
-// the 8-row template: measured 0.4-2.9 % faster than a 6-row one on C1, C4
-// and the 5120^2 / 4096 -> 12288 layers (one cell +0.1 %).  The owner-fold
-// kernel keeps a 6-row template (its 8-row instance: 42.2-42.5 us at 7-8 rows
-// of 16 x 4096 -> 1024 K5 against 40.1 us for the 6-row one at 5-6).
-static uint32_t rows_template(uint64_t rows) { return rows <= 4 ? uint32_t(rows ? rows : 1) : 8; }
-static uint32_t owner_rows_template(uint64_t rows) { return rows <= 6 && rows > 4 ? 6 : rows_template(rows); }
+// Row template of a call: rows are computed in groups of 1, 2, 4 or 8 (the
+// rows past the call's are zero inputs whose results are never stored).  A
+// row's arithmetic does not depend on the template.  Measured against
+// templates of their own: three rows run 2.6-7 % faster on the 4-row one
+// (C1 neutral), five and six rows 0.4-2.9 % faster on the 8-row one (one cell
+// +0.1 %).  The owner-fold kernel keeps 3- and 6-row templates (its 8-row
+// instance: 42.2-42.5 us at 7-8 rows of 16 x 4096 -> 1024 K5 against 40.1 us
+// for the 6-row one at 5-6).
+static uint32_t rows_template(uint64_t rows) { return rows <= 2 ? uint32_t(rows ? rows : 1) : rows <= 4 ? 4 : 8; }
+static uint32_t owner_rows_template(uint64_t rows) {
+    return rows == 3 ? 3 : rows == 5 || rows == 6 ? 6 : rows_template(rows);
+}
 
 using GemvDispatch = hipError_t (*)(const GemvLaunch&);
 static const GemvDispatch gemv_table[8] = {gemv_dispatch<1>, gemv_dispatch<2>, gemv_dispatch<3>,

@@ -729,12 +729,12 @@ void gemv_kernel(const uint32_t* trellis, const uint16_t* suh, const float* x0, 
     // together (each batch is one memory round trip; one unit at a time made
     // the 8-row input stage six round trips long).  The first batch is issued
     // before the weight prefetch, so waiting for it does not wait for the
-    // weights.  (Four units in flight make the 3- and 4-row mcg / 3inst
-    // kernels spill, so those keep two.)
+    // weights.  (Four units in flight make the 4-row mcg / 3inst kernels
+    // spill, so those keep two.)
     // The 2- and 8-row templates' work item is a pair of units, one per
     // 32-lane half (input_load_quad): the same units per wave and batch from a
     // quarter of the load instructions.  (Measured: 3-5 % faster at 7-8 rows
-    // and up to 5.6 % at 2 rows; mixed at 3-4 rows, where single units stay.)
+    // and up to 5.6 % at 2 rows; mixed at 4 rows, where single units stay.)
     constexpr bool kQuadIn = RT == 2 * GEMV_WAVES || RT == 2;
     using Unit = std::conditional_t<kQuadIn, InputQuad, InputLoad>;
     constexpr int kUnits = (RT <= 2 ? 2 : RT <= 4 ? (CB == CB_MUL1 ? 4 : 2) : 8) / (kQuadIn ? 2 : 1);
@@ -1062,7 +1062,7 @@ __global__ __launch_bounds__(64) void decode_kernel(const uint32_t* trellis, uin
 struct GemvLaunch {
     GemvArgs args;
     dim3 grid;
-    uint32_t rows_template;   // 1, 2, 3, 4 or 8 (the owner-fold kernel also 6)
+    uint32_t rows_template;   // 1, 2, 4 or 8 (the owner-fold kernel also 3 and 6)
     uint32_t codebook;
     size_t lds;
     hipStream_t stream;
@@ -1082,16 +1082,13 @@ hipError_t decode_dispatch(uint32_t codebook, const uint32_t* trellis, uint32_t 
     hipError_t gemv_dispatch<K>(const GemvLaunch& l) {                                                    \
         using Fn = void (*)(const uint32_t*, const uint16_t*, const float*, uint32_t*, const GroupWeights*,  \
                             uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, GemvArgs);                   \
-        static const Fn table[3][5] = {                                                                   \
-            {gemv_kernel<K, 0, 1>, gemv_kernel<K, 0, 2>, gemv_kernel<K, 0, 3>, gemv_kernel<K, 0, 4>,      \
-             gemv_kernel<K, 0, 8>},                                                                       \
-            {gemv_kernel<K, 1, 1>, gemv_kernel<K, 1, 2>, gemv_kernel<K, 1, 3>, gemv_kernel<K, 1, 4>,      \
-             gemv_kernel<K, 1, 8>},                                                                       \
-            {gemv_kernel<K, 2, 1>, gemv_kernel<K, 2, 2>, gemv_kernel<K, 2, 3>, gemv_kernel<K, 2, 4>,      \
-             gemv_kernel<K, 2, 8>}};                                                                      \
+        static const Fn table[3][4] = {                                                                   \
+            {gemv_kernel<K, 0, 1>, gemv_kernel<K, 0, 2>, gemv_kernel<K, 0, 4>, gemv_kernel<K, 0, 8>},     \
+            {gemv_kernel<K, 1, 1>, gemv_kernel<K, 1, 2>, gemv_kernel<K, 1, 4>, gemv_kernel<K, 1, 8>},     \
+            {gemv_kernel<K, 2, 1>, gemv_kernel<K, 2, 2>, gemv_kernel<K, 2, 4>, gemv_kernel<K, 2, 8>}};    \
         const int rt = int(l.rows_template);                                                              \
-        if (rt != 8 && (rt < 1 || rt > 4)) return hipErrorInvalidValue;                                  \
-        const int ri = rt <= 4 ? rt - 1 : 4;                                                              \
+        if (rt != 1 && rt != 2 && rt != 4 && rt != 8) return hipErrorInvalidValue;                       \
+        const int ri = rt <= 2 ? rt - 1 : rt == 4 ? 2 : 3;                                                \
         const GemvArgs& a = l.args;                                                                       \
         if (a.ncg > 0xFFFFu || a.groups > 0xFFFFu || a.bps > 0xFFFFu || a.splits > 0xFFFFu ||             \
             a.rows > 0xFFu || a.mode > 0xFFu || a.x_row_stride > 0xFFFFFFFFull)                           \

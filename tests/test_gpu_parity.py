@@ -188,8 +188,8 @@ def test_rows_plans_and_entry_points_bit_identical(ctx, I, N, K):
         assert torch.equal(yp.view(torch.int32), y8.view(torch.int32))
     assert plan.launches() == 1
     plan.destroy()
-    # 2 rows (2-row template), 3 rows (3-row template) and 5, 6 or 7 rows
-    # (8-row template with dead rows) keep their bits
+    # 2 rows (2-row template), 3 rows (4-row template with a dead row) and 5, 6
+    # or 7 rows (8-row template with dead rows) keep their bits
     for rows in (2, 3, 5, 6, 7):
         yr = torch.empty((rows, N), device=DEV)
         runtime.gemv(w, x[:rows].contiguous(), yr)
