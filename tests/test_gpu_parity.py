@@ -168,7 +168,13 @@ def test_gemv_core_within_fp64_tolerance(ctx):
 def test_rows_plans_and_entry_points_bit_identical(ctx, I, N, K):
     print(f"row invariance {I}x{N} K={K}", flush=True)
     w, (tr, suh, svh, b) = _weights(ctx, I, N, K, 5 + K, bias=True)
-    x = torch.from_numpy(synth.activations(8, I, 3)).to(DEV)
+    # RN16 ties, subnormals and signed zeros in row 0 and, reversed, in rows 1
+    # and 5: the 2- and 8-row templates take even rows in lanes 0-31 and odd
+    # rows in lanes 32-63, so both halves see them.
+    xs = _special_x(8, I, 3)
+    xs[1] = xs[0][::-1]
+    xs[5] = xs[0][::-1]
+    x = torch.from_numpy(np.ascontiguousarray(xs)).to(DEV)
     y8 = torch.empty((8, N), device=DEV)
     runtime.gemv(w, x, y8)
     singles = []
